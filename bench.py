@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""bench.py — routed-MoE decode layer on one MI355X.
+
+One step = one routed-MoE layer at decode: device gating of N(0,1) logits over
+256 experts (top-8, sigmoid weights renormalised), then the expert-indexed
+MXFP4 grouped GEMV (routing tables, stage A = W1/W3 + SiLU, stage B = W2 +
+weighted combine) reading the routed experts in place from HBM-resident
+per-layer tensors. Inputs are resident in HBM before the timed region. Steps
+cycle over --layers layers of 256 experts (4 x 3.42 GB by default) with fresh
+logits each step, so weights come from HBM, not the 256 MB MALL.
+
+Prints ONE JSON line. `value` is the layer's algorithmic HBM bytes per step
+(unique routed experts x 13,369,344 B + activations + routing) divided by the
+step time, in GB/s. `roofline` covers the dominant kernel (stage A), timed
+alone over back-to-back launches with HIP events. `cpu_baseline` times the
+CPU oracle (dequant + fp32 matmul, the reference's CPU path) on one step.
+
+    python bench.py [--steps K] [--warmup W] [--tokens T] [--layers L]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "dsv4-flash-gb10-runtime_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "MoE-layer decode µs + MXFP4 grouped GEMV HBM GB/s (% of MI355X peak)"
+HBM_PEAK_GBS = 8000.0
+E, K, H, O, TOPK = 256, 4096, 2048, 4096, 8
+EXPERT_BYTES = 3 * (H * K // 2 + H * K // 32)          # 13,369,344 B (W1 + W3 + W2, packed + scales)
+STAGE_A_EXPERT_BYTES = 2 * (H * K // 2 + H * K // 32)  # 8,912,896 B (W1 + W3)
+STAGE_B_EXPERT_BYTES = O * H // 2 + O * H // 32         # 4,456,448 B (W2)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def topk_ids(logits: np.ndarray) -> np.ndarray:
+    return np.argsort(-logits.astype(np.float64), axis=1, kind="stable")[:, :TOPK]
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--tokens", type=int, default=1, help="decode tokens per step (config 3: 1, 4, 16)")
+    ap.add_argument("--layers", type=int, default=4, help="resident layers cycled over (MALL defeat)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on one GPU only: this build has no multi-GPU path "
+              "(the routed MoE would shard by experts or by the ff dimension; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from runtime import moe, synth
+    from runtime import mxfp4_grouped_gemv_binding as gb
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    T, L = args.tokens, args.layers
+    n_steps = args.warmup + args.steps
+
+    log(f"allocating {L} layers x {E} experts ({L * E * EXPERT_BYTES / 1e9:.2f} GB)")
+    layers = [moe.make_moe_weights(20000 + 100 * l, E, K, H, O, dev) for l in range(L)]
+    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=max(16, T)) for w in layers]
+    x = torch.from_numpy(synth.normal_bf16(3001, (T, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+    logits_h = synth.gating_logits(3002, n_steps * T, E).reshape(n_steps, T, E)
+    logits = torch.from_numpy(logits_h).to(dev)
+    torch.cuda.synchronize()
+
+    uniq = np.array([len(np.unique(topk_ids(logits_h[i]))) for i in range(n_steps)])
+    step_bytes = uniq * EXPERT_BYTES + 2 * T * K * 2 + T * TOPK * 8 + T * E * 4
+
+    def step(i: int):
+        return mods[i % L].forward(x, logits=logits[i])
+
+    log(f"warmup {args.warmup} steps, T={T}")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"timing {args.steps} steps")
+    ev0.record()
+    for i in range(args.warmup, n_steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    timed_bytes = float(step_bytes[args.warmup:].mean())
+    value = timed_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # --- dominant kernel alone: stage A (W1/W3 + SiLU), back-to-back launches ---
+    R = min(64, n_steps)
+    stages = []
+    for i in range(R):
+        st = gb.MoEStages(layers[i % L].W1, layers[i % L].W3, layers[i % L].W2, T, TOPK, dev)
+        ids, w = gb.route_sigmoid_topk(logits[i], TOPK)
+        st.build_routing(ids, w)
+        stages.append(st)
+    out = torch.empty(T, O, dtype=torch.bfloat16, device=dev)
+    for st in stages:
+        st.swiglu(x)
+        st.down(out)
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // R)
+    log(f"timing stage A alone: {reps * R} launches")
+    ev0.record()
+    for _ in range(reps):
+        for st in stages:
+            st.swiglu(x)
+    ev1.record()
+    torch.cuda.synchronize()
+    a_us = ev0.elapsed_time(ev1) * 1e3 / (reps * R)
+    ev0.record()
+    for _ in range(reps):
+        for st in stages:
+            st.down(out)
+    ev1.record()
+    torch.cuda.synchronize()
+    b_us = ev0.elapsed_time(ev1) * 1e3 / (reps * R)
+    a_bytes = float(np.mean(uniq[:R] * STAGE_A_EXPERT_BYTES + T * K * 2 + T * TOPK * H * 2))
+    b_bytes = float(np.mean(uniq[:R] * STAGE_B_EXPERT_BYTES + T * TOPK * H * 2 + T * O * 2))
+    a_gbs = a_bytes / (a_us * 1e-6) / 1e9
+
+    # --- CPU baseline: the oracle (dequant + fp32 matmul) on step 0's experts ---
+    cpu = None
+    if not args.no_cpu_baseline:
+        from threadpoolctl import threadpool_info, threadpool_limits
+
+        from oracle import mx
+
+        ids0 = topk_ids(logits_h[0])
+        lw = layers[0]
+        cache = {}
+
+        def expert(e):
+            if e not in cache:
+                cache[e] = tuple((m["packed"][e].cpu().numpy(), m["scale"][e].cpu().numpy())
+                                 for m in (lw.W1, lw.W3, lw.W2))
+            return cache[e]
+
+        ids_t, w_t = mx.route_sigmoid_topk(logits_h[0], TOPK)
+        xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
+        for e in np.unique(ids_t):
+            expert(int(e))
+        threads = min(os.cpu_count() or 1, 16)
+        with threadpool_limits(limits=threads):
+            blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+            log(f"cpu baseline: oracle moe layer, {threads} BLAS threads")
+            t0 = time.perf_counter()
+            n_calls = 0
+            while True:
+                mx.moe_layer(xh, expert, ids_t, w_t, O)
+                n_calls += 1
+                if time.perf_counter() - t0 > 10.0 or n_calls >= 3:
+                    break
+            cpu_s = (time.perf_counter() - t0) / n_calls
+        cpu = {
+            "value": round(float(step_bytes[0]) / cpu_s / 1e9, 4),
+            "unit": "GB/s",
+            "us_per_layer": round(cpu_s * 1e6, 1),
+            "cores": int(blas[0]) if blas else threads,
+            "kind": "port",
+            "sample": (f"{n_calls} call(s) of the numpy oracle moe_layer (unpack + E8M0 scale -> "
+                       f"bf16 dequant, fp32 matmul, bf16 casts) on step 0: T={T}, "
+                       f"{len(np.unique(ids_t))} routed experts of layer 0; host {cpu_model()}, "
+                       f"nproc {os.cpu_count()}"),
+        }
+        del ids0
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4-e2m1/e8m0 weights, bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded SplitMix64 weights filled on device, N(0,1) activations/logits)",
+        "config": {
+            "workload": f"configs[3]: routed MoE layer decode, T={T}, top-{TOPK} of {E} MXFP4 experts "
+                        f"(W1/W3 {H}x{K}, W2 {O}x{H}), device sigmoid gating, {L} resident layers",
+            "tokens": T, "experts": E, "topk": TOPK, "layers_cycled": L,
+            "mean_unique_experts": round(float(uniq[args.warmup:].mean()), 3),
+            "algorithmic_bytes_per_step": int(round(timed_bytes)),
+        },
+        "moe_layer_us": round(ms_per_step * 1e3, 3),
+        "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        "stage_us": {"swiglu_A": round(a_us, 3), "down_B": round(b_us, 3)},
+        "roofline": {
+            "kernel": "moe_swiglu_kernel (stage A: W1+W3 MXFP4 GEMV + SiLU)",
+            "bound": "hbm",
+            "achieved": round(a_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(a_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": int(round(a_bytes)),
+            "avg_launch_us": round(a_us, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

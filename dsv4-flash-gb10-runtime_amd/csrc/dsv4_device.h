@@ -1,0 +1,184 @@
+// dsv4_device.h — device helpers shared by the gfx950 decode kernels.
+//
+// Number formats (OCP Microscaling Formats v1.0):
+//   e2m1  : 4-bit code s.ee.m, values {0, .5, 1, 1.5, 2, 3, 4, 6} with sign;
+//           code 8 is -0.0. Two codes per byte, low nibble = even element
+//           (reference runtime/mxfp4_unpack.py:105-112).
+//   E8M0  : scale byte b -> 2^(b-127); b == 0xFF decodes to 0.0 on the kernel
+//           path (reference kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:74-78),
+//           b == 0 gives the fp32 subnormal 2^-127 exactly (no flush).
+//   E4M3FN: 1.4.3, bias 7, no infinities, 0x7F/0xFF NaN, subnormals m*2^-9.
+//
+// Decode uses the gfx950 conversion instructions v_cvt_scalef32_pk_bf16_fp4 /
+// _fp8 with a unit scale, which map each code to its exact bf16 value; the
+// E8M0 block scale is applied once per block in fp32 (exact power of two).
+// Dot products use v_dot2_f32_bf16 (two bf16 products added into an fp32
+// accumulator), so one 16-byte MXFP4 block costs 16 conversions + 16 dots.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsv4 {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- scalars --
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+    return __uint_as_float(b << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0 (sign kept).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// E8M0 byte -> fp32 scale, kernel convention (0xFF -> 0, 0 -> 2^-127).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
+    uint32_t bits = (b == 0u) ? 0x00400000u : (b << 23);
+    bits = (b == 0xFFu) ? 0u : bits;
+    return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t u) {
+    return __builtin_bit_cast(bf16x2, u);
+}
+
+__device__ __forceinline__ uint32_t as_u32(bf16x2 v) {
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Two e2m1 codes of byte SEL of w -> bf16 pair {low nibble, high nibble}.
+template <int SEL>
+__device__ __forceinline__ bf16x2 fp4x2_to_bf16x2(uint32_t w) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, SEL);
+}
+
+// Two E4M3FN bytes (low half-word when HI == false) -> bf16 pair.
+template <bool HI>
+__device__ __forceinline__ bf16x2 fp8x2_to_bf16x2(uint32_t w) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+}
+
+__device__ __forceinline__ float dot2(bf16x2 a, bf16x2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+}
+
+// ------------------------------------------------------------- block dots --
+
+// Sum over one 32-element MXFP4 block (16 packed bytes in w) of code * x,
+// with x given as 16 packed bf16 pairs (element order 2p, 2p+1 in pair p).
+// The caller multiplies by the block's E8M0 scale.
+__device__ __forceinline__ float fp4_block_dot(const u32x4 w, const uint32_t* xp) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = w[i];
+        a0 = dot2(fp4x2_to_bf16x2<0>(d), as_bf16x2(xp[4 * i + 0]), a0);
+        a1 = dot2(fp4x2_to_bf16x2<1>(d), as_bf16x2(xp[4 * i + 1]), a1);
+        a0 = dot2(fp4x2_to_bf16x2<2>(d), as_bf16x2(xp[4 * i + 2]), a0);
+        a1 = dot2(fp4x2_to_bf16x2<3>(d), as_bf16x2(xp[4 * i + 3]), a1);
+    }
+    return a0 + a1;
+}
+
+// Sum over 16 E4M3 bytes (w) of e4m3 * x, x as 8 packed bf16 pairs.
+__device__ __forceinline__ float fp8_chunk_dot(const u32x4 w, const uint32_t* xp) {
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = w[i];
+        a0 = dot2(fp8x2_to_bf16x2<false>(d), as_bf16x2(xp[2 * i + 0]), a0);
+        a1 = dot2(fp8x2_to_bf16x2<true>(d), as_bf16x2(xp[2 * i + 1]), a1);
+    }
+    return a0 + a1;
+}
+
+// ---------------------------------------------------------------- loads ----
+
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Streaming (read-once) 16-byte load of weight data.
+__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// 16-byte load without any alignment assumption (byte loads).
+__device__ __forceinline__ u32x4 ld16_unaligned(const uint8_t* p) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = (uint32_t)p[4 * i] | ((uint32_t)p[4 * i + 1] << 8) |
+               ((uint32_t)p[4 * i + 2] << 16) | ((uint32_t)p[4 * i + 3] << 24);
+    return r;
+}
+
+// ----------------------------------------------------------- reductions ----
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+// Butterfly reduction of N values per lane over the 64 lanes of a wave
+// (N a power of two, N <= 64). Each exchange step halves the number of live
+// values, so N sums cost about N + 5 shuffles instead of 6N. On return every
+// lane holds in v[0] the wave total of value index (lane >> (6 - log2 N)).
+template <int N>
+struct WaveButterfly {
+    static __device__ __forceinline__ void run(float* v, int lane, int mask) {
+        constexpr int H = N / 2;
+        const bool upper = (lane & mask) != 0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float send = upper ? v[i] : v[i + H];
+            const float keep = upper ? v[i + H] : v[i];
+            v[i] = keep + __shfl_xor(send, mask, kWave);
+        }
+        WaveButterfly<H>::run(v, lane, mask >> 1);
+    }
+};
+template <>
+struct WaveButterfly<1> {
+    static __device__ __forceinline__ void run(float* v, int, int mask) {
+#pragma unroll
+        for (; mask > 0; mask >>= 1) v[0] += __shfl_xor(v[0], mask, kWave);
+    }
+};
+
+template <int N>
+__device__ __forceinline__ void wave_reduce_n(float* v, int lane) {
+    WaveButterfly<N>::run(v, lane, 32);
+}
+
+template <int N>
+struct Log2 { static constexpr int value = 1 + Log2<N / 2>::value; };
+template <>
+struct Log2<1> { static constexpr int value = 0; };
+
+// Index of the value whose total lane `lane` holds after wave_reduce_n<N>.
+template <int N>
+__device__ __forceinline__ int reduced_index(int lane) {
+    return lane >> (6 - Log2<N>::value);
+}
+// True for exactly one lane per value index after wave_reduce_n<N>.
+template <int N>
+__device__ __forceinline__ bool reduced_owner(int lane) {
+    return (lane & ((1 << (6 - Log2<N>::value)) - 1)) == 0;
+}
+
+__device__ __forceinline__ float silu_f32(float g) {
+    return g / (1.0f + __expf(-g));
+}
+
+}  // namespace dsv4

@@ -1,0 +1,235 @@
+// fp8_e4m3_gemv.hip — FP8 E4M3FN GEMV with 128x128 E8M0 tile scales, gfx950.
+//
+//   y[t,n] = bf16( sum_k e4m3(W[n,k]) * 2^(S[n/128,k/128]-127) * x[t,k] )
+//
+// Wave layout: lane l owns the 16-byte chunks k = 1024*j + 16*l of every row
+// it visits (one wave-wide load = 1 KiB of a row, coalesced), so each chunk
+// lies inside one 128-column scale tile. E4M3FN bytes are decoded with
+// v_cvt_scalef32_pk_bf16_fp8 (OCP e4m3fn on gfx950, exact in bf16),
+// multiplied against the bf16 activation pairs with v_dot2_f32_bf16 in fp32,
+// and the tile scale is applied once per chunk. kRows rows per wave are
+// reduced together with one butterfly. N need not be a multiple of 128
+// (ceil(N/128) scale rows), unlike reference kernel/fp8-dense/fp8_e4m3_gemv.cu:148-154.
+
+#include <cstdio>
+
+#include "dsv4_device.h"
+#include "dsv4_kernels.h"
+
+namespace {
+
+using namespace dsv4;
+
+constexpr int kTile = 128;
+constexpr int kMaxK = 16384;    // reference FP8_GEMV_MAX_K (fp8_e4m3_gemv.cu:48-50)
+constexpr int kMaxT = 16;
+constexpr int kWaves = 4;
+constexpr int kRows = 4;
+
+struct Fp8Args {
+    const uint16_t* x;
+    int64_t xstride;            // elements between token rows of x
+    const uint8_t* w;
+    const uint8_t* s;
+    int K;
+    int N;
+    int T;
+    int64_t wrow;
+    int64_t srow;
+    uint16_t* y;
+    int64_t ystride;            // elements between token rows of y
+};
+
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load_w16(const uint8_t* p) {
+    if constexpr (ALIGNED) return ld16(p);
+    else return ld16_unaligned(p);
+}
+
+// grid = ceil(N / (kWaves*kRows)), block = 64*kWaves. A row is walked in
+// segments of NC*1024 bytes (NC 16-byte chunks per lane, NC <= 4). With one
+// segment (K <= 4096) the rows stay in registers across all T tokens;
+// longer rows are re-streamed per token.
+template <int NC, bool ALIGNED>
+__global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * kWaves + wave) * kRows;
+    if (n0 >= a.N) return;
+    const int nseg = (a.K + NC * 1024 - 1) / (NC * 1024);
+
+    u32x4 wv[kRows][NC];
+    float sc[kRows][NC];
+    auto load_rows = [&](int seg) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const int n = n0 + r;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int k = (seg * NC + j) * 1024 + 16 * lane;
+                if (n < a.N && k < a.K) {
+                    wv[r][j] = load_w16<ALIGNED>(a.w + (int64_t)n * a.wrow + k);
+                    sc[r][j] = e8m0_to_f32(a.s[(int64_t)(n / kTile) * a.srow + k / kTile]);
+                } else {
+                    wv[r][j] = u32x4{0u, 0u, 0u, 0u};
+                    sc[r][j] = 0.f;
+                }
+            }
+        }
+    };
+    auto accumulate = [&](const uint16_t* xt, int seg, float* acc) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            uint32_t xp[8];
+            const int k = (seg * NC + j) * 1024 + 16 * lane;
+            if (k < a.K) {
+                if constexpr (ALIGNED) {
+                    const u32x4* s4 = reinterpret_cast<const u32x4*>(xt + k);
+                    const u32x4 v0 = s4[0], v1 = s4[1];
+                    xp[0] = v0[0]; xp[1] = v0[1]; xp[2] = v0[2]; xp[3] = v0[3];
+                    xp[4] = v1[0]; xp[5] = v1[1]; xp[6] = v1[2]; xp[7] = v1[3];
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        xp[q] = (uint32_t)xt[k + 2 * q] | ((uint32_t)xt[k + 2 * q + 1] << 16);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) xp[q] = 0u;
+            }
+#pragma unroll
+            for (int r = 0; r < kRows; ++r)
+                acc[r] = fmaf(fp8_chunk_dot(wv[r][j], xp), sc[r][j], acc[r]);
+        }
+    };
+    if (nseg == 1) load_rows(0);
+    for (int t = 0; t < a.T; ++t) {
+        const uint16_t* xt = a.x + (int64_t)t * a.xstride;
+        float acc[kRows];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
+        if (nseg == 1) {
+            accumulate(xt, 0, acc);
+        } else {
+            for (int seg = 0; seg < nseg; ++seg) {
+                load_rows(seg);
+                accumulate(xt, seg, acc);
+            }
+        }
+        wave_reduce_n<kRows>(acc, lane);
+        const int r = reduced_index<kRows>(lane);
+        if (reduced_owner<kRows>(lane) && n0 + r < a.N)
+            a.y[(int64_t)t * a.ystride + n0 + r] = f32_to_bf16_bits(acc[0]);
+    }
+}
+
+// One thread per 16 bytes of a row.
+__global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* w, const uint8_t* s, int K,
+                                                          int N, int64_t wrow, int64_t srow,
+                                                          uint16_t* out) {
+    const int nchunk = K / 16;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)N * nchunk) return;
+    const int n = (int)(idx / nchunk);
+    const int k = (int)(idx % nchunk) * 16;
+    const u32x4 v = ld16_unaligned(w + (int64_t)n * wrow + k);
+    const float sc = e8m0_to_f32(s[(int64_t)(n / kTile) * srow + k / kTile]);
+    uint16_t* o = out + (int64_t)n * K + k;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = as_u32(fp8x2_to_bf16x2<false>(v[i]));
+        const uint32_t hi = as_u32(fp8x2_to_bf16x2<true>(v[i]));
+        o[4 * i + 0] = f32_to_bf16_bits(bf16_bits_to_f32(lo & 0xFFFFu) * sc);
+        o[4 * i + 1] = f32_to_bf16_bits(bf16_bits_to_f32(lo >> 16) * sc);
+        o[4 * i + 2] = f32_to_bf16_bits(bf16_bits_to_f32(hi & 0xFFFFu) * sc);
+        o[4 * i + 3] = f32_to_bf16_bits(bf16_bits_to_f32(hi >> 16) * sc);
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int validate(int K, int N) {
+    if (K % kTile != 0 || K < kTile) {
+        std::fprintf(stderr, "fp8_e4m3_gemv: K=%d not a positive multiple of %d\n", K, kTile);
+        return -1;
+    }
+    if (K > kMaxK) {
+        std::fprintf(stderr, "fp8_e4m3_gemv: K=%d > %d\n", K, kMaxK);
+        return -3;
+    }
+    if (N < 1) {
+        std::fprintf(stderr, "fp8_e4m3_gemv: N=%d < 1\n", N);
+        return -4;
+    }
+    return 0;
+}
+
+int launch(const Fp8Args& a, hipStream_t stream) {
+    const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) &&
+                    (a.T == 1 || a.xstride % 8 == 0);
+    const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)));
+    const dim3 block(64 * kWaves);
+    const int nc = (a.K + 1023) / 1024;
+#define DSV4_LAUNCH(NCV)                                                                    \
+    if (al) hipLaunchKernelGGL((fp8_gemv_kernel<NCV, true>), grid, block, 0, stream, a);   \
+    else hipLaunchKernelGGL((fp8_gemv_kernel<NCV, false>), grid, block, 0, stream, a);
+    switch (nc) {
+        case 1: DSV4_LAUNCH(1) break;
+        case 2: DSV4_LAUNCH(2) break;
+        case 3: DSV4_LAUNCH(3) break;
+        default: DSV4_LAUNCH(4) break;
+    }
+#undef DSV4_LAUNCH
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "fp8_e4m3_gemv launch failed: %s\n", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int fp8_e4m3_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_fp8, const uint8_t* W_scale,
+                                int K, int N, int64_t weight_row_stride_bytes,
+                                int64_t scale_row_stride_bytes, dsv4_bf16_t* y, hipStream_t stream) {
+    const int v = validate(K, N);
+    if (v != 0) return v;
+    Fp8Args a{reinterpret_cast<const uint16_t*>(x), K, W_fp8, W_scale, K, N, 1,
+              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y), N};
+    return launch(a, stream);
+}
+
+extern "C" int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
+                             const uint8_t* W_scale, int K, int N, int T,
+                             int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                             dsv4_bf16_t* y, int64_t y_row_stride, hipStream_t stream) {
+    const int v = validate(K, N);
+    if (v != 0) return v;
+    if (T < 1 || T > kMaxT) {
+        std::fprintf(stderr, "fp8_e4m3_gemv: T=%d outside [1, %d]\n", T, kMaxT);
+        return -5;
+    }
+    Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W_fp8, W_scale, K, N, T,
+              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y),
+              y_row_stride};
+    return launch(a, stream);
+}
+
+extern "C" int fp8_e4m3_dequant_bf16(const uint8_t* W_fp8, const uint8_t* W_scale, int K, int N,
+                                     int64_t weight_row_stride_bytes,
+                                     int64_t scale_row_stride_bytes, dsv4_bf16_t* out,
+                                     hipStream_t stream) {
+    if (K % kTile != 0 || K < kTile) return -1;
+    if (N < 1) return -4;
+    const int64_t total = (int64_t)N * (K / 16);
+    hipLaunchKernelGGL(fp8_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       stream, W_fp8, W_scale, K, N, weight_row_stride_bytes,
+                       scale_row_stride_bytes, reinterpret_cast<uint16_t*>(out));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "fp8_e4m3_dequant_bf16 launch failed: %s\n", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}

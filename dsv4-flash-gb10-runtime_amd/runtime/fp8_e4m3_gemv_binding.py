@@ -1,0 +1,131 @@
+"""ctypes binding of libfp8_e4m3_gemv.so (FP8 E4M3FN GEMV, 128x128 E8M0 tiles).
+
+Drop-in API (call contract of the reference runtime/fp8_e4m3_gemv_binding.py:77-168):
+
+    fp8_e4m3_gemv(W_fp8 [N, K] u8, W_scale [ceil(N/128), K/128] u8, x [K] bf16,
+                  out=None, stream=None) -> y [N] bf16
+
+Differences, both extensions: N need not be a multiple of 128 (the reference
+raises for it), and x may be [T, K] with T <= 16, in which case one launch
+streams W once for all T tokens and y is [T, N].
+
+Extension (debug): fp8_e4m3_dequant(W_fp8, W_scale) -> [N, K] bf16.
+
+Errors: RuntimeError for device/dtype/shape problems and for a non-zero
+return code. The library path is $FP8_E4M3_GEMV_LIB or
+kernel/fp8-dense/libfp8_e4m3_gemv.so.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+FP8_BLOCK_TILE = 128
+MAX_TOKENS = 16
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def lib_path() -> str:
+    return _lib.lib_path("FP8_E4M3_GEMV_LIB", "fp8-dense", "libfp8_e4m3_gemv.so")
+
+
+def _load_lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        lib = _lib.load(lib_path())
+        P, I, L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+        lib.fp8_e4m3_gemv_m1.argtypes = [P, P, P, I, I, L, L, P, P]
+        lib.fp8_e4m3_gemv_m1.restype = I
+        lib.fp8_e4m3_gemv.argtypes = [P, L, P, P, I, I, I, L, L, P, L, P]
+        lib.fp8_e4m3_gemv.restype = I
+        lib.fp8_e4m3_dequant_bf16.argtypes = [P, P, I, I, L, L, P, P]
+        lib.fp8_e4m3_dequant_bf16.restype = I
+        _LIB = lib
+    return _LIB
+
+
+def _check_w(W_fp8: torch.Tensor, W_scale: torch.Tensor) -> None:
+    if not (W_fp8.is_cuda and W_scale.is_cuda):
+        raise RuntimeError("all tensors must be on a GPU device")
+    if W_fp8.dtype != torch.uint8:
+        raise RuntimeError(f"W_fp8 must be uint8 (raw E4M3), got {W_fp8.dtype}")
+    if W_scale.dtype != torch.uint8:
+        raise RuntimeError(f"W_scale must be uint8 (raw E8M0), got {W_scale.dtype}")
+    if W_fp8.dim() != 2:
+        raise RuntimeError(f"W_fp8 must be 2-D [N, K], got shape {tuple(W_fp8.shape)}")
+    if W_scale.dim() != 2:
+        raise RuntimeError(f"W_scale must be 2-D [ceil(N/128), K/128], got {tuple(W_scale.shape)}")
+    if W_fp8.stride(1) != 1 or W_scale.stride(1) != 1:
+        raise RuntimeError("W_fp8 / W_scale rows must be contiguous (row stride is free)")
+    N, K = W_fp8.shape
+    if K % FP8_BLOCK_TILE != 0:
+        raise RuntimeError(f"K={K} must be a multiple of {FP8_BLOCK_TILE}")
+    want = ((N + FP8_BLOCK_TILE - 1) // FP8_BLOCK_TILE, K // FP8_BLOCK_TILE)
+    if tuple(W_scale.shape) != want:
+        raise RuntimeError(f"W_scale shape {tuple(W_scale.shape)} != {want} "
+                           f"(one E8M0 byte per 128x128 tile)")
+
+
+def fp8_e4m3_gemv(
+    W_fp8: torch.Tensor,
+    W_scale: torch.Tensor,
+    x: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    stream: Optional[torch.cuda.Stream] = None,
+) -> torch.Tensor:
+    """y = x @ dequant(W).T for x [K] (y [N]) or x [T, K] (y [T, N]); fp32 accumulate."""
+    _check_w(W_fp8, W_scale)
+    if not x.is_cuda:
+        raise RuntimeError("all tensors must be on a GPU device")
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError(f"x must be bfloat16, got {x.dtype}")
+    if x.dim() not in (1, 2):
+        raise RuntimeError(f"x must be [K] or [T, K], got shape {tuple(x.shape)}")
+    N, K = W_fp8.shape
+    if x.shape[-1] != K:
+        raise RuntimeError(f"x last dim {x.shape[-1]} != K={K}")
+    T = 1 if x.dim() == 1 else x.shape[0]
+    if T > MAX_TOKENS:
+        raise RuntimeError(f"T={T} > {MAX_TOKENS}")
+    x = x.contiguous()
+    oshape = (N,) if x.dim() == 1 else (T, N)
+    if out is None:
+        out = torch.empty(oshape, dtype=torch.bfloat16, device=x.device)
+    elif tuple(out.shape) != oshape or out.dtype != torch.bfloat16 or not out.is_cuda \
+            or not out.is_contiguous():
+        raise RuntimeError(f"out must be a contiguous GPU bfloat16 {oshape} tensor")
+    s = ctypes.c_void_p(_lib.stream_ptr(x.device, stream))
+    lib = _load_lib()
+    if x.dim() == 1:
+        rc = lib.fp8_e4m3_gemv_m1(_lib.vp(x), _lib.vp(W_fp8), _lib.vp(W_scale), K, N,
+                                  W_fp8.stride(0), W_scale.stride(0), _lib.vp(out), s)
+        name = "fp8_e4m3_gemv_m1"
+    else:
+        rc = lib.fp8_e4m3_gemv(_lib.vp(x), K, _lib.vp(W_fp8), _lib.vp(W_scale), K, N, T,
+                               W_fp8.stride(0), W_scale.stride(0), _lib.vp(out), N, s)
+        name = "fp8_e4m3_gemv"
+    if rc != 0:
+        raise RuntimeError(f"{name} returned {rc}")
+    return out
+
+
+def fp8_e4m3_dequant(W_fp8: torch.Tensor, W_scale: torch.Tensor,
+                     stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """[N, K] bf16 = e4m3(W) * 2^(S[n/128, k/128] - 127), decoded on the GPU."""
+    _check_w(W_fp8, W_scale)
+    N, K = W_fp8.shape
+    out = torch.empty(N, K, dtype=torch.bfloat16, device=W_fp8.device)
+    rc = _load_lib().fp8_e4m3_dequant_bf16(
+        _lib.vp(W_fp8), _lib.vp(W_scale), K, N, W_fp8.stride(0), W_scale.stride(0), _lib.vp(out),
+        ctypes.c_void_p(_lib.stream_ptr(W_fp8.device, stream)))
+    if rc != 0:
+        raise RuntimeError(f"fp8_e4m3_dequant_bf16 returned {rc}")
+    return out
+
+
+__all__ = ["fp8_e4m3_gemv", "fp8_e4m3_dequant", "FP8_BLOCK_TILE"]

@@ -1,0 +1,268 @@
+"""ctypes binding of libmxfp4_grouped_gemv.so (routed MXFP4 SwiGLU MoE).
+
+Drop-in API (same call contract as the reference binding
+runtime/mxfp4_grouped_gemv_binding.py:95-174):
+
+    mxfp4_grouped_gemv(W1, W3, W2, scales, x, r) -> out [out_dim] bf16
+
+    W1, W3: {'packed': uint8 [n_exp, hidden, K_in/2], 'scale': uint8 [n_exp, hidden, K_in/32]}
+    W2:     {'packed': uint8 [n_exp, out_dim, hidden/2], 'scale': uint8 [n_exp, out_dim, hidden/32]}
+    scales: ignored (the scales live in W{1,3,2}['scale'])
+    x:      bf16 [K_in];  r: float32 [n_exp]
+
+Extensions (not in the reference):
+
+    route_sigmoid_topk(logits [T, E] f32, topk) -> (ids [T, topk] int32, weights [T, topk] f32)
+    mxfp4_moe_grouped_gemv(x [T, K_in], W1, W3, W2, ids, weights, out=None, workspace=None)
+        experts read in place from per-layer tensors [n_experts, ...].
+
+Errors: ValueError for device/dtype/shape/contiguity problems, RuntimeError for
+a non-zero return code of the library. The library path is
+$MXFP4_GROUPED_LIB or kernel/mxfp4-routed/libmxfp4_grouped_gemv.so.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+MXFP4_BLOCK_ELEMS = 32
+
+_c_int, _c_void_p, _c_size_t = ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def lib_path() -> str:
+    return _lib.lib_path("MXFP4_GROUPED_LIB", "mxfp4-routed", "libmxfp4_grouped_gemv.so")
+
+
+def _load_lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    lib = _lib.load(lib_path())
+    lib.mxfp4_grouped_gemv_topk.restype = _c_int
+    lib.mxfp4_grouped_gemv_topk.argtypes = [_c_void_p] * 8 + [_c_int] * 4 + [_c_void_p] * 3
+    lib.mxfp4_grouped_workspace_bytes.restype = _c_size_t
+    lib.mxfp4_grouped_workspace_bytes.argtypes = [_c_int] * 3
+    lib.mxfp4_moe_route_sigmoid_topk.restype = _c_int
+    lib.mxfp4_moe_route_sigmoid_topk.argtypes = [_c_void_p, _c_int, _c_int, _c_int,
+                                                 _c_void_p, _c_void_p, _c_void_p]
+    lib.mxfp4_moe_workspace_bytes.restype = _c_size_t
+    lib.mxfp4_moe_workspace_bytes.argtypes = [_c_int] * 4
+    lib.mxfp4_moe_grouped_gemv.restype = _c_int
+    lib.mxfp4_moe_grouped_gemv.argtypes = ([_c_void_p] * 9 + [_c_int] * 6 + [_c_void_p] * 3)
+    lib.mxfp4_moe_build_routing.restype = _c_int
+    lib.mxfp4_moe_build_routing.argtypes = [_c_void_p] * 2 + [_c_int] * 4 + [_c_void_p] * 2
+    lib.mxfp4_moe_swiglu.restype = _c_int
+    lib.mxfp4_moe_swiglu.argtypes = [_c_void_p] * 5 + [_c_int] * 5 + [_c_void_p] * 2
+    lib.mxfp4_moe_down.restype = _c_int
+    lib.mxfp4_moe_down.argtypes = [_c_void_p] * 2 + [_c_int] * 5 + [_c_void_p] * 3
+    _LIB = lib
+    return lib
+
+
+def _check(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name}: expected a GPU tensor, got device={t.device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+
+
+def _check_mats(W1, W3, W2) -> None:
+    for name, w in (("W1", W1), ("W3", W3), ("W2", W2)):
+        if "packed" not in w or "scale" not in w:
+            raise ValueError(f"{name} must contain 'packed' and 'scale' tensors")
+        _check(w["packed"], f"{name}.packed", torch.uint8)
+        _check(w["scale"], f"{name}.scale", torch.uint8)
+        if w["packed"].dim() != 3 or w["scale"].dim() != 3:
+            raise ValueError(f"{name}: packed/scale must be 3-D [experts, rows, cols]")
+
+
+def _shapes(W1, W3, W2, K_in: int) -> Tuple[int, int, int]:
+    n_exp, hidden = W1["packed"].shape[0], W1["packed"].shape[1]
+    out_dim = W2["packed"].shape[1]
+    if tuple(W3["packed"].shape) != tuple(W1["packed"].shape):
+        raise ValueError(f"W3.packed shape {tuple(W3['packed'].shape)} != W1.packed shape "
+                         f"{tuple(W1['packed'].shape)}")
+    if W1["packed"].shape[2] != K_in // 2:
+        raise ValueError(f"W1.packed last dim {W1['packed'].shape[2]} != K_in/2={K_in // 2}")
+    want = (n_exp, hidden, K_in // MXFP4_BLOCK_ELEMS)
+    if tuple(W1["scale"].shape) != want or tuple(W3["scale"].shape) != want:
+        raise ValueError(f"W1/W3.scale shape must be {want}")
+    if W2["packed"].shape[0] != n_exp or W2["packed"].shape[2] != hidden // 2:
+        raise ValueError(f"W2.packed shape {tuple(W2['packed'].shape)} != "
+                         f"({n_exp}, out_dim, {hidden // 2})")
+    want2 = (n_exp, out_dim, hidden // MXFP4_BLOCK_ELEMS)
+    if tuple(W2["scale"].shape) != want2:
+        raise ValueError(f"W2.scale shape {tuple(W2['scale'].shape)} != {want2}")
+    return n_exp, hidden, out_dim
+
+
+def workspace_bytes(n_exp: int, hidden: int, out_dim: int) -> int:
+    return int(_load_lib().mxfp4_grouped_workspace_bytes(n_exp, hidden, out_dim))
+
+
+def mxfp4_grouped_gemv(
+    W1: Dict[str, torch.Tensor],
+    W3: Dict[str, torch.Tensor],
+    W2: Dict[str, torch.Tensor],
+    scales: Any,
+    x: torch.Tensor,
+    r: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Routed SwiGLU over the n_exp packed experts for one token; returns bf16 [out_dim].
+
+    `out` and `workspace` may be passed to avoid per-call allocation (the
+    reference allocates both on every call).
+    """
+    del scales
+    lib = _load_lib()
+    _check(x, "x", torch.bfloat16)
+    _check(r, "r", torch.float32)
+    _check_mats(W1, W3, W2)
+    K_in = x.numel()
+    n_exp, hidden, out_dim = _shapes(W1, W3, W2, K_in)
+    if tuple(r.shape) != (n_exp,):
+        raise ValueError(f"r shape {tuple(r.shape)} != ({n_exp},)")
+    if out is None:
+        out = torch.empty(out_dim, dtype=torch.bfloat16, device=x.device)
+    else:
+        _check(out, "out", torch.bfloat16)
+        if out.numel() != out_dim:
+            raise ValueError(f"out numel {out.numel()} != {out_dim}")
+    ws_bytes = lib.mxfp4_grouped_workspace_bytes(n_exp, hidden, out_dim)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace smaller than {ws_bytes} bytes")
+    rc = lib.mxfp4_grouped_gemv_topk(
+        _lib.vp(x), _lib.vp(W1["packed"]), _lib.vp(W3["packed"]), _lib.vp(W2["packed"]),
+        _lib.vp(W1["scale"]), _lib.vp(W3["scale"]), _lib.vp(W2["scale"]), _lib.vp(r),
+        K_in, hidden, out_dim, n_exp, _lib.vp(out), _lib.vp(workspace),
+        ctypes.c_void_p(_lib.stream_ptr(x.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_grouped_gemv_topk returned {rc}")
+    return out
+
+
+def route_sigmoid_topk(logits: torch.Tensor, topk: int,
+                       ids: Optional[torch.Tensor] = None,
+                       weights: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Device gating: top-k of logits [T, E] with sigmoid weights renormalised to 1."""
+    lib = _load_lib()
+    _check(logits, "logits", torch.float32)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [T, n_experts]")
+    T, E = logits.shape
+    if ids is None:
+        ids = torch.empty(T, topk, dtype=torch.int32, device=logits.device)
+    if weights is None:
+        weights = torch.empty(T, topk, dtype=torch.float32, device=logits.device)
+    _check(ids, "ids", torch.int32)
+    _check(weights, "weights", torch.float32)
+    rc = lib.mxfp4_moe_route_sigmoid_topk(_lib.vp(logits), T, E, topk, _lib.vp(ids),
+                                          _lib.vp(weights),
+                                          ctypes.c_void_p(_lib.stream_ptr(logits.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_route_sigmoid_topk returned {rc}")
+    return ids, weights
+
+
+def moe_workspace_bytes(T: int, topk: int, n_experts: int, hidden: int) -> int:
+    return int(_load_lib().mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden))
+
+
+def mxfp4_moe_grouped_gemv(
+    x: torch.Tensor,
+    W1: Dict[str, torch.Tensor],
+    W3: Dict[str, torch.Tensor],
+    W2: Dict[str, torch.Tensor],
+    ids: torch.Tensor,
+    weights: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Expert-indexed routed SwiGLU for T tokens; returns bf16 [T, out_dim]."""
+    lib = _load_lib()
+    _check(x, "x", torch.bfloat16)
+    _check(ids, "ids", torch.int32)
+    _check(weights, "weights", torch.float32)
+    _check_mats(W1, W3, W2)
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    T, K_in = x.shape
+    n_experts, hidden, out_dim = _shapes(W1, W3, W2, K_in)
+    if ids.dim() != 2 or ids.shape[0] != T or tuple(weights.shape) != tuple(ids.shape):
+        raise ValueError(f"ids/weights must both be [T={T}, topk]")
+    topk = ids.shape[1]
+    if out is None:
+        out = torch.empty(T, out_dim, dtype=torch.bfloat16, device=x.device)
+    else:
+        _check(out, "out", torch.bfloat16)
+        if out.numel() != T * out_dim:
+            raise ValueError(f"out numel {out.numel()} != {T * out_dim}")
+    ws_bytes = lib.mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace smaller than {ws_bytes} bytes")
+    rc = lib.mxfp4_moe_grouped_gemv(
+        _lib.vp(x), _lib.vp(W1["packed"]), _lib.vp(W3["packed"]), _lib.vp(W2["packed"]),
+        _lib.vp(W1["scale"]), _lib.vp(W3["scale"]), _lib.vp(W2["scale"]),
+        _lib.vp(ids), _lib.vp(weights), T, topk, n_experts, K_in, hidden, out_dim,
+        _lib.vp(out), _lib.vp(workspace), ctypes.c_void_p(_lib.stream_ptr(x.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_grouped_gemv returned {rc}")
+    return out
+
+
+class MoEStages:
+    """The three launches of mxfp4_moe_grouped_gemv, callable one by one on a
+    fixed workspace (preallocated here): build_routing(ids, weights) ->
+    swiglu(x) -> down(out)."""
+
+    def __init__(self, W1, W3, W2, T: int, topk: int, device):
+        self.lib = _load_lib()
+        _check_mats(W1, W3, W2)
+        self.W1, self.W3, self.W2 = W1, W3, W2
+        self.n_experts, self.hidden = W1["packed"].shape[0], W1["packed"].shape[1]
+        self.K = W1["packed"].shape[2] * 2
+        self.out_dim = W2["packed"].shape[1]
+        self.T, self.topk = T, topk
+        ws = self.lib.mxfp4_moe_workspace_bytes(T, topk, self.n_experts, self.hidden)
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device=device)
+
+    def _rc(self, name: str, rc: int) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{name} returned {rc}")
+
+    def build_routing(self, ids: torch.Tensor, weights: torch.Tensor) -> None:
+        self._rc("mxfp4_moe_build_routing", self.lib.mxfp4_moe_build_routing(
+            _lib.vp(ids), _lib.vp(weights), self.T, self.topk, self.n_experts, self.hidden,
+            _lib.vp(self.workspace), ctypes.c_void_p(_lib.stream_ptr(ids.device))))
+
+    def swiglu(self, x: torch.Tensor) -> None:
+        self._rc("mxfp4_moe_swiglu", self.lib.mxfp4_moe_swiglu(
+            _lib.vp(x), _lib.vp(self.W1["packed"]), _lib.vp(self.W3["packed"]),
+            _lib.vp(self.W1["scale"]), _lib.vp(self.W3["scale"]), self.T, self.topk,
+            self.n_experts, self.K, self.hidden, _lib.vp(self.workspace),
+            ctypes.c_void_p(_lib.stream_ptr(x.device))))
+
+    def down(self, out: torch.Tensor) -> torch.Tensor:
+        self._rc("mxfp4_moe_down", self.lib.mxfp4_moe_down(
+            _lib.vp(self.W2["packed"]), _lib.vp(self.W2["scale"]), self.T, self.topk,
+            self.n_experts, self.hidden, self.out_dim, _lib.vp(out), _lib.vp(self.workspace),
+            ctypes.c_void_p(_lib.stream_ptr(out.device))))
+        return out
+
+
+__all__ = ["mxfp4_grouped_gemv", "MoEStages", "MXFP4_BLOCK_ELEMS", "route_sigmoid_topk",
+           "mxfp4_moe_grouped_gemv", "moe_workspace_bytes", "workspace_bytes"]

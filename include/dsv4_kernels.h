@@ -1,0 +1,201 @@
+/*
+ * dsv4_kernels.h — C ABI of the MI355X (gfx950) quantized decode kernels.
+ *
+ * Four shared libraries export these symbols under the reference's file names,
+ * so a caller that dlopen()s / ctypes-loads the reference .so files can load
+ * these instead:
+ *
+ *   kernel/mxfp4-routed/libmxfp4_grouped_gemv.so  mxfp4_grouped_gemv_topk,
+ *                                                 mxfp4_grouped_workspace_bytes,
+ *                                                 mxfp4_moe_* (extensions)
+ *   kernel/mxfp4-dense/libmxfp4_gemv.so           mxfp4_gemv_m1,
+ *                                                 mxfp4_dequant_bf16 (extension)
+ *   kernel/fp8-dense/libfp8_e4m3_gemv.so          fp8_e4m3_gemv_m1,
+ *                                                 fp8_e4m3_gemv, fp8_e4m3_dequant_bf16
+ *                                                 (extensions)
+ *   kernel/rmsnorm-fuse/librmsnorm_fuse.so        rmsnorm_fuse_fwd,
+ *                                                 rmsnorm_fuse_residual_add
+ *
+ * Conventions shared by every entry point:
+ *   - every pointer is a device pointer; the caller owns every buffer
+ *     (the kernels never allocate device memory);
+ *   - bf16 tensors are passed as raw 16-bit storage (dsv4_bf16_t);
+ *   - `stream` is a hipStream_t (an opaque pointer; ctypes passes c_void_p);
+ *   - host-side validation runs before any launch and returns the reference's
+ *     error codes; only launch errors are detected (no device sync).
+ *
+ * MXFP4 layout (OCP MX v1.0): e2m1 codes packed two per byte, low nibble =
+ * even element, high nibble = odd element; one E8M0 scale byte per 32
+ * contiguous K-elements, scale = 2^(byte-127), byte 0xFF decodes to 0.0.
+ * FP8 layout: one E4M3FN byte per element, one E8M0 byte per 128x128 tile.
+ */
+#ifndef DSV4_KERNELS_H
+#define DSV4_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t dsv4_bf16_t;
+
+/* ------------------------------------------------------------------------ */
+/* libmxfp4_grouped_gemv.so                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Routed SwiGLU MoE for one decode token over n_exp packed experts:
+ *   out = bf16( sum_e rweights[e] * W2_e . bf16( silu(W1_e x) * (W3_e x) ) )
+ * Layouts: W1/W3 packed [n_exp, hidden, K_in/2], scales [n_exp, hidden, K_in/32];
+ * W2 packed [n_exp, out_dim, hidden/2], scale [n_exp, out_dim, hidden/32].
+ * Returns 0; -1 K_in%32 or K_in < 32; -2 hidden%32 or hidden < 32; -3 K_in or
+ * hidden > 4096; -4 n_exp outside [1, 256] (the reference accepts only its
+ * compiled-in 6); -5/-6 launch failure of stage A/B, also out_dim < 1 (-6).
+ * Replaces mxfp4_grouped_gemv_topk, reference
+ * kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:294-310. */
+int mxfp4_grouped_gemv_topk(const dsv4_bf16_t* x,
+                            const uint8_t* W1_packed, const uint8_t* W3_packed,
+                            const uint8_t* W2_packed,
+                            const uint8_t* W1_scale, const uint8_t* W3_scale,
+                            const uint8_t* W2_scale,
+                            const float* rweights,
+                            int K_in, int hidden, int out_dim, int n_exp,
+                            dsv4_bf16_t* out, void* workspace, hipStream_t stream);
+
+/* Workspace bytes for mxfp4_grouped_gemv_topk: n_exp*hidden*2 + out_dim*4
+ * (the same formula as the reference, so caller-side preallocation matches).
+ * Replaces kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:406-409. */
+size_t mxfp4_grouped_workspace_bytes(int n_exp, int hidden, int out_dim);
+
+/* EXTENSION (no reference counterpart; the reference routes on the host,
+ * kernel/cpp-engine-mxfp4/routed.cu:169-208). Device-side gating for T tokens:
+ * ids[t, :] = top-`topk` expert indices of logits[t, :] (descending, ties to
+ * the lower index); weights[t, k] = sigmoid(l_k) / sum_k' sigmoid(l_k').
+ * Returns 0; -1 bad T/n_experts/topk (T<1, n_experts<1 or >1024, topk<1 or
+ * > min(n_experts, 16)); -5 launch failure. */
+int mxfp4_moe_route_sigmoid_topk(const float* logits, int T, int n_experts, int topk,
+                                 int32_t* ids, float* weights, hipStream_t stream);
+
+/* EXTENSION: workspace bytes for mxfp4_moe_grouped_gemv. */
+size_t mxfp4_moe_workspace_bytes(int T, int topk, int n_experts, int hidden);
+
+/* EXTENSION (reference runs T single-token calls after 36 D2D pack copies,
+ * kernel/cpp-engine-mxfp4/routed.cu:266-283, runtime/dsv4_engine_mxfp4.py:412-423).
+ * Expert-indexed multi-token routed SwiGLU MoE: experts are read in place from
+ * per-layer tensors W1/W3 [n_experts, hidden, K_in/2], W2 [n_experts, out_dim,
+ * hidden/2] (+ scales), each unique routed expert is streamed once for all of
+ * its tokens; one launch per projection (stage A: W1+W3, stage B: W2).
+ *   out[t] = bf16( sum_k weights[t,k] * W2_{ids[t,k]} . bf16(silu(W1 x_t) * (W3 x_t)) )
+ * x [T, K_in] bf16, ids/weights [T, topk], out [T, out_dim] bf16.
+ * Returns 0; -1 K_in%32; -2 hidden%32; -3 K_in/hidden > 4096; -4 bad
+ * T/topk/n_experts (T<1 or >64, topk<1 or >16, n_experts<1 or >1024);
+ * -5/-6/-7 launch failure of routing/stage A/stage B. An id outside
+ * [0, n_experts) is skipped (contributes nothing). */
+int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x,
+                           const uint8_t* W1_packed, const uint8_t* W3_packed,
+                           const uint8_t* W2_packed,
+                           const uint8_t* W1_scale, const uint8_t* W3_scale,
+                           const uint8_t* W2_scale,
+                           const int32_t* ids, const float* weights,
+                           int T, int topk, int n_experts,
+                           int K_in, int hidden, int out_dim,
+                           dsv4_bf16_t* out, void* workspace, hipStream_t stream);
+
+/* EXTENSION: the three launches of mxfp4_moe_grouped_gemv as separate entry
+ * points (same arguments and workspace), for callers that schedule or overlap
+ * the projections themselves and for per-launch timing:
+ *   mxfp4_moe_build_routing: device routing tables from ids/weights (1 launch);
+ *   mxfp4_moe_swiglu:        stage A, W1/W3 + SiLU -> bf16 intermediate in the
+ *                            workspace (1 launch);
+ *   mxfp4_moe_down:          stage B, W2 + weighted combine -> out (1 launch).
+ * They must run in this order on one stream with one workspace sized by
+ * mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden). Return codes as
+ * mxfp4_moe_grouped_gemv. */
+int mxfp4_moe_build_routing(const int32_t* ids, const float* weights, int T, int topk,
+                            int n_experts, int hidden, void* workspace, hipStream_t stream);
+int mxfp4_moe_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed, const uint8_t* W3_packed,
+                     const uint8_t* W1_scale, const uint8_t* W3_scale, int T, int topk,
+                     int n_experts, int K_in, int hidden, void* workspace, hipStream_t stream);
+int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int topk,
+                   int n_experts, int hidden, int out_dim, dsv4_bf16_t* out, void* workspace,
+                   hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* libmxfp4_gemv.so                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* y[n] = bf16( sum_k dequant(W)[n,k] * x[k] ), W packed [N, K/2] with row
+ * stride packed_row_stride_bytes, scales [N, K/32] with row stride
+ * scale_row_stride_bytes. Returns 0; -1 K%32 or K < 32; -2 K > 8192; -3 launch
+ * failure, also N < 1 (the reference's zero-size grid fails its launch).
+ * Replaces mxfp4_gemv_m1, reference kernel/mxfp4-dense/mxfp4_gemv.cu:131-166. */
+int mxfp4_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_packed, const uint8_t* W_scale,
+                  int K, int N, int64_t packed_row_stride_bytes,
+                  int64_t scale_row_stride_bytes, dsv4_bf16_t* y, hipStream_t stream);
+
+/* EXTENSION (debug): out[n,k] = bf16( e2m1(W[n,k]) * 2^(S[n,k/32]-127) ), using
+ * the same device decode routine as the GEMVs, so a bit-exact comparison with
+ * the reference dequant (runtime/mxfp4_loader.py:272-309) checks the kernels'
+ * decode. out is [N, K] contiguous. Returns 0; -1 K%32; -3 launch failure. */
+int mxfp4_dequant_bf16(const uint8_t* W_packed, const uint8_t* W_scale, int K, int N,
+                       int64_t packed_row_stride_bytes, int64_t scale_row_stride_bytes,
+                       dsv4_bf16_t* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* libfp8_e4m3_gemv.so                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* y[n] = bf16( sum_k e4m3(W[n,k]) * 2^(S[n/128, k/128]-127) * x[k] ).
+ * W [N, K] bytes (row stride weight_row_stride_bytes), S [ceil(N/128), K/128]
+ * (row stride scale_row_stride_bytes). Returns 0; -1 K%128 or K < 128;
+ * -3 K > 16384; -4 launch failure, also N < 1 (the reference's zero-size grid
+ * fails its launch). N need not be a multiple of 128: the reference returns -2
+ * there (kernel/fp8-dense/fp8_e4m3_gemv.cu:148-154); this build accepts it so
+ * the 576-row projection runs, with ceil(N/128) scale rows.
+ * Replaces fp8_e4m3_gemv_m1, reference kernel/fp8-dense/fp8_e4m3_gemv.cu:132-174. */
+int fp8_e4m3_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_fp8, const uint8_t* W_scale,
+                     int K, int N, int64_t weight_row_stride_bytes,
+                     int64_t scale_row_stride_bytes, dsv4_bf16_t* y, hipStream_t stream);
+
+/* EXTENSION (reference loops fp8_e4m3_gemv_m1 per token,
+ * runtime/dsv4_engine_mxfp4.py:310-319): T-token FP8 GEMV that streams W once.
+ * x [T, K] (row stride x_row_stride elements), y [T, N] (row stride
+ * y_row_stride elements). Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16. */
+int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
+                  const uint8_t* W_scale, int K, int N, int T,
+                  int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                  dsv4_bf16_t* y, int64_t y_row_stride, hipStream_t stream);
+
+/* EXTENSION (debug): out[n,k] = bf16( e4m3(W[n,k]) * 2^(S[n/128,k/128]-127) ),
+ * the device decode of the FP8 GEMVs, for the bit-exact check against
+ * runtime/dsv4_engine_mxfp4.py:531-553. Returns 0; -1 K%128; -4 launch failure. */
+int fp8_e4m3_dequant_bf16(const uint8_t* W_fp8, const uint8_t* W_scale, int K, int N,
+                          int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                          dsv4_bf16_t* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* librmsnorm_fuse.so                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* y[r,h] = bf16( w[h] * x[r,h] * rsqrt(mean_h(x[r,:]^2) + eps) ), bf16 in/out.
+ * Returns 0 (also for n_rows <= 0 or hidden <= 0: no-op); 1 hidden > 8192;
+ * otherwise a hipError_t from the launch.
+ * Replaces rmsnorm_fuse_fwd, reference kernel/rmsnorm-fuse/rmsnorm_fuse.cu:161-182. */
+int rmsnorm_fuse_fwd(const void* x, const void* weight, void* y, int n_rows, int hidden,
+                     float eps, hipStream_t stream);
+
+/* t = x + residual (fp32); new_residual = bf16(t);
+ * y_norm = bf16( w * bf16(t) * rsqrt(sum(t^2)/hidden + eps) ). Return codes as
+ * rmsnorm_fuse_fwd.
+ * Replaces rmsnorm_fuse_residual_add, reference rmsnorm_fuse.cu:184-209. */
+int rmsnorm_fuse_residual_add(const void* x, const void* residual, const void* weight,
+                              void* y_norm, void* new_residual, int n_rows, int hidden,
+                              float eps, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4_KERNELS_H */

@@ -1,0 +1,290 @@
+"""numpy restatement of the reference's CPU math for the decode hot path.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py). Every function names the
+reference file:line it restates and how it is pinned (checked against
+something independent of this file). bf16 values travel as uint16 bit
+patterns; float32 is the working precision of the reference path
+("dequant -> bf16 -> fp32 matmul -> bf16").
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ------------------------------------------------------------------ bf16 ----
+
+
+def bf16_round(a) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (torch's .to(torch.bfloat16)).
+
+    Pinned: tests compare with torch.Tensor.to(torch.bfloat16) on random, tie,
+    subnormal, inf and NaN inputs."""
+    a = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    u = a.view(np.uint32).astype(np.uint64)
+    is_nan = (u & 0x7FFFFFFF) > 0x7F800000
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) & 0xFFFF
+    r = np.where(is_nan, ((u >> 16) | 0x40) & 0xFFFF, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------- number formats --
+
+
+def e2m1_value(code) -> np.ndarray:
+    """e2m1 code (0..15) -> value: sign bit 3, exponent bits 2..1, mantissa bit 0;
+    exponent 0 is subnormal (m * 0.5), otherwise 2^(e-1) * (1 + m/2).
+    Restates the codebook of runtime/mxfp4_unpack.py:36-39 (OCP MX v1.0).
+
+    Pinned: tests compare all 16 codes with the OCP MX v1.0 FP4 table and with
+    torch.float4_e2m1fn_x2 where that dtype converts."""
+    c = np.asarray(code, dtype=np.int64)
+    s = (c >> 3) & 1
+    e = (c >> 1) & 3
+    m = c & 1
+    mag = np.where(e == 0, 0.5 * m, np.ldexp(1.0 + 0.5 * m, (e - 1).astype(np.int32)))
+    return np.where(s == 1, -mag, mag).astype(np.float32)
+
+
+E2M1_TABLE = e2m1_value(np.arange(16))
+
+
+def e8m0_decode(b, kernel_convention: bool = True) -> np.ndarray:
+    """E8M0 byte -> fp32 scale 2^(b-127) (runtime/e8m0_decode.py:32-64).
+    Byte 0xFF is NaN in the Python reference and 0.0 in the reference kernels
+    (kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:74-78,
+    kernel/mxfp4-dense/mxfp4_gemv.cu:65-69); `kernel_convention` picks which.
+    Byte 0 gives the fp32 subnormal 2^-127.
+
+    Pinned: tests compare all 256 bytes with torch.float8_e8m0fnu and math.ldexp."""
+    b = np.asarray(b, dtype=np.uint8)
+    e = b.astype(np.int32) - 127
+    v = np.ldexp(np.float64(1.0), np.where(b == 0xFF, 0, e)).astype(np.float32)
+    return np.where(b == 0xFF, np.float32(0.0 if kernel_convention else np.nan), v)
+
+
+def e4m3fn_decode(b) -> np.ndarray:
+    """E4M3FN byte -> fp32: sign.eeee.mmm, bias 7, exponent 0 subnormal
+    (m * 2^-9), 0x7F / 0xFF NaN, no infinities (torch.float8_e4m3fn, as used by
+    runtime/dsv4_engine_mxfp4.py:539-540).
+
+    Pinned: tests compare all 256 bytes with torch.float8_e4m3fn."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int64)
+    s = (b >> 7) & 1
+    e = (b >> 3) & 15
+    m = b & 7
+    mag = np.where(e == 0, np.ldexp(m.astype(np.float64), -9),
+                   np.ldexp(1.0 + m / 8.0, (e - 7).astype(np.int32)))
+    mag = np.where((e == 15) & (m == 7), np.nan, mag)
+    return np.where(s == 1, -mag, mag).astype(np.float32)
+
+
+# ------------------------------------------------------------- MXFP4 pack ---
+
+
+def mxfp4_unpack(packed, shape, dtype=np.float32) -> np.ndarray:
+    """Flat packed bytes -> codebook values in `shape`; low nibble = element 2i,
+    high nibble = element 2i+1 (runtime/mxfp4_unpack.py:93-118).
+
+    Pinned: known-answer bytes written from the packing rule and an exhaustive
+    pack/unpack round trip in the tests."""
+    flat = np.ascontiguousarray(np.asarray(packed, dtype=np.uint8)).reshape(-1)
+    if flat.size * 2 != int(np.prod(shape)):
+        raise ValueError(f"{flat.size} bytes -> {flat.size * 2} nibbles != prod{tuple(shape)}")
+    codes = np.empty(flat.size * 2, dtype=np.uint8)
+    codes[0::2] = flat & 0x0F
+    codes[1::2] = flat >> 4
+    return E2M1_TABLE[codes].astype(dtype).reshape(shape)
+
+
+def mxfp4_pack(values) -> np.ndarray:
+    """Inverse of mxfp4_unpack for values exactly in the codebook; -0.0 packs to
+    code 8 and +0.0 to code 0 (runtime/mxfp4_unpack.py:121-168)."""
+    v = np.asarray(values, dtype=np.float64).reshape(-1)
+    if v.size % 2:
+        raise ValueError("element count must be even")
+    mag = np.abs(v)
+    mags = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+    idx = np.searchsorted(mags, mag)
+    idx = idx.clip(0, 7)
+    if not np.all(mags[idx] == mag):
+        bad = np.nonzero(mags[idx] != mag)[0][0]
+        raise ValueError(f"value {v[bad]} at index {bad} not in the e2m1 codebook")
+    codes = (idx | (np.signbit(v).astype(np.int64) << 3)).astype(np.uint8)
+    return ((codes[1::2] << 4) | codes[0::2]).astype(np.uint8)
+
+
+def mxfp4_dequant_bf16(packed, scale, kernel_convention: bool = True) -> np.ndarray:
+    """[N, K/2] packed + [N, K/32] E8M0 -> [N, K] bf16 bits:
+    bf16(code_f32 * 2^(s-127)) per 32-element block
+    (runtime/mxfp4_loader.py:272-309: unpack fp32, view [N, K/32, 32] times the
+    decoded scale, .to(bfloat16)). Every product is exact in fp32, so the only
+    rounding is the final bf16 cast.
+
+    Pinned: tests compare with products of torch.float8_e8m0fnu scales and the
+    OCP code table converted by torch, and against the scalar C oracle."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    scale = np.asarray(scale, dtype=np.uint8)
+    N, kh = packed.shape
+    K = kh * 2
+    if scale.shape != (N, K // 32):
+        raise ValueError(f"scale shape {scale.shape} != {(N, K // 32)}")
+    vals = mxfp4_unpack(packed, (N, K // 32, 32))
+    s = e8m0_decode(scale, kernel_convention)[:, :, None]
+    with np.errstate(over="ignore"):  # code 6 x 2^127 overflows to inf, as in torch
+        return bf16_round((vals * s).reshape(N, K))
+
+
+def fp8_dequant_bf16(w, s, kernel_convention: bool = True) -> np.ndarray:
+    """[N, K] E4M3FN + [ceil(N/128), K/128] E8M0 -> [N, K] bf16 bits:
+    bf16(e4m3(w) * 2^(S[n/128, k/128]-127)) (runtime/dsv4_engine_mxfp4.py:531-553;
+    the repeat_interleave + crop there equals indexing the tile by n//128, k//128).
+
+    Pinned: tests compare with torch's float8_e4m3fn / float8_e8m0fnu views and
+    against the scalar C oracle."""
+    w = np.asarray(w, dtype=np.uint8)
+    s = np.asarray(s, dtype=np.uint8)
+    N, K = w.shape
+    sf = e8m0_decode(s, kernel_convention)
+    full = np.repeat(np.repeat(sf, 128, axis=0), 128, axis=1)[:N, :K]
+    with np.errstate(over="ignore", invalid="ignore"):
+        return bf16_round(e4m3fn_decode(w) * full)
+
+
+# ------------------------------------------------------------------ GEMVs ---
+
+
+def _matvec_f32(W_bf16, x_bf16) -> np.ndarray:
+    """fp32 product of bf16 operands: y[..., n] = sum_k W[n,k] x[..., k]."""
+    return (bf16_to_f32(x_bf16) @ bf16_to_f32(W_bf16).T).astype(np.float32)
+
+
+def mxfp4_gemv(x, packed, scale) -> np.ndarray:
+    """y = bf16( dequant(W) @ x ) with fp32 accumulation
+    (kernel/mxfp4-dense/mxfp4_gemv.cu:72-128 via its bit-exact reference
+    mxfp4_unpack + e8m0_decode + torch matmul, mxfp4_gemv.cu:33).
+    x: bf16 bits [K] or [T, K]."""
+    return bf16_round(_matvec_f32(mxfp4_dequant_bf16(packed, scale), x))
+
+
+def fp8_gemv(x, w, s) -> np.ndarray:
+    """y = bf16( x @ dequant(W).T ) with fp32 accumulation
+    (runtime/fp8_e4m3_gemv_binding.py:84 contract, dequant of
+    runtime/dsv4_engine_mxfp4.py:531-553). x: bf16 bits [K] or [T, K]."""
+    return bf16_round(_matvec_f32(fp8_dequant_bf16(w, s), x))
+
+
+def silu_f32(v) -> np.ndarray:
+    """x / (1 + exp(-x)) in fp32 (kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:122-124)."""
+    v = np.asarray(v, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return (v / (np.float32(1.0) + np.exp(-v))).astype(np.float32)
+
+
+def expert_swiglu_m(x, W1p, W1s, W3p, W3s) -> np.ndarray:
+    """M = bf16( silu(W1 x) * (W3 x) ) for one expert, fp32 math
+    (kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:186-208, the bf16 rounding at :208).
+    x: bf16 bits [K] or [T, K]."""
+    g = _matvec_f32(mxfp4_dequant_bf16(W1p, W1s), x)
+    u = _matvec_f32(mxfp4_dequant_bf16(W3p, W3s), x)
+    return bf16_round(silu_f32(g) * u)
+
+
+def grouped_gemv_topk(x, W1p, W3p, W2p, W1s, W3s, W2s, r) -> np.ndarray:
+    """Routed SwiGLU for one token over n_exp packed experts:
+    out = bf16( sum_e r[e] * (W2_e @ M_e) ), fp32 accumulation in expert order
+    (kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:143-289; the reference adds the
+    experts with fp32 atomics in arbitrary order).
+    Shapes: x [K]; W1p/W3p [n, H, K/2]; W2p [n, O, H/2]; scales [.., /32]; r [n]."""
+    r = np.asarray(r, dtype=np.float32)
+    acc = np.zeros(W2p.shape[1], dtype=np.float32)
+    for e in range(W1p.shape[0]):
+        M = expert_swiglu_m(x, W1p[e], W1s[e], W3p[e], W3s[e])
+        y = _matvec_f32(mxfp4_dequant_bf16(W2p[e], W2s[e]), M)
+        acc = (acc + r[e] * y).astype(np.float32)
+    return bf16_round(acc)
+
+
+def moe_layer(x, expert_fn, ids, weights, out_dim: int) -> np.ndarray:
+    """out[t] = bf16( sum_k w[t,k] * W2_e . bf16(silu(W1_e x_t) * (W3_e x_t)) ),
+    e = ids[t,k] (runtime/dsv4_engine_mxfp4.py:372-423 with the grouped kernel
+    per token). expert_fn(e) -> ((W1p, W1s), (W3p, W3s), (W2p, W2s)).
+    Each unique expert is dequantised once. Ids outside [0, E) are skipped."""
+    x = np.atleast_2d(np.asarray(x, dtype=np.uint16))
+    ids = np.asarray(ids)
+    weights = np.asarray(weights, dtype=np.float32)
+    T = x.shape[0]
+    acc = np.zeros((T, out_dim), dtype=np.float32)
+    for e in np.unique(ids):
+        tok, kk = np.nonzero(ids == e)
+        (W1p, W1s), (W3p, W3s), (W2p, W2s) = expert_fn(int(e))
+        M = expert_swiglu_m(x[tok], W1p, W1s, W3p, W3s)
+        y = _matvec_f32(mxfp4_dequant_bf16(W2p, W2s), M)
+        for i, t in enumerate(tok):
+            acc[t] = (acc[t] + weights[t, kk[i]] * y[i]).astype(np.float32)
+    return bf16_round(acc)
+
+
+def route_sigmoid_topk(logits, topk: int):
+    """Config gating: top-k logits per token (descending, ties to the lower
+    index), weights sigmoid(l) / sum sigmoid over the top-k. The reference's own
+    gating (sqrt-softplus x 1.5, runtime/dsv4_engine_mxfp4.py:363-370) differs;
+    the benchmark configuration prescribes this one.
+
+    Pinned: tests compare with torch.topk and torch.sigmoid."""
+    l = np.asarray(logits, dtype=np.float32)
+    ids = np.argsort(-l.astype(np.float64), axis=1, kind="stable")[:, :topk].astype(np.int32)
+    sel = np.take_along_axis(l, ids, axis=1).astype(np.float64)
+    s = 1.0 / (1.0 + np.exp(-sel))
+    return ids, (s / s.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- RMSNorm ---
+
+
+def rmsnorm(x, w, eps: float = 1e-6) -> np.ndarray:
+    """y = bf16( (w * x) * rsqrt(sum(x^2)/H + eps) ) per row
+    (kernel/rmsnorm-fuse/rmsnorm_fuse.cu:86-103; runtime/dsv4_engine_mxfp4.py:136-141
+    computes the same up to product order). Sum of squares in fp64."""
+    xf = bf16_to_f32(np.atleast_2d(x)).astype(np.float64)
+    H = xf.shape[-1]
+    rms = 1.0 / np.sqrt((xf * xf).sum(axis=-1, keepdims=True) / H + eps)
+    wf = bf16_to_f32(w).astype(np.float64)
+    return bf16_round((wf * xf) * rms)
+
+
+def rmsnorm_residual(x, r, w, eps: float = 1e-6):
+    """t = x + r (fp32, exact for bf16 inputs of similar magnitude);
+    new_residual = bf16(t); y = bf16( (w * bf16(t)) * rsqrt(sum(t^2)/H + eps) )
+    with the sum over the unrounded t (kernel/rmsnorm-fuse/rmsnorm_fuse.cu:135-156).
+    Returns (y, new_residual) as bf16 bits. Sum of squares in fp64."""
+    t = (bf16_to_f32(np.atleast_2d(x)) + bf16_to_f32(np.atleast_2d(r))).astype(np.float32)
+    new_res = bf16_round(t)
+    td = t.astype(np.float64)
+    H = td.shape[-1]
+    rms = 1.0 / np.sqrt((td * td).sum(axis=-1, keepdims=True) / H + eps)
+    wf = bf16_to_f32(w).astype(np.float64)
+    y = bf16_round((wf * bf16_to_f32(new_res).astype(np.float64)) * rms)
+    return y, new_res
+
+
+# --------------------------------------------------------------- metrics ----
+
+
+def compare(got_bits, ref_bits):
+    """(max relative error, cosine) of two bf16 tensors, in fp64:
+    rel = max|got - ref| / max|ref| and cosine over the flattened values."""
+    g = bf16_to_f32(got_bits).astype(np.float64).reshape(-1)
+    r = bf16_to_f32(ref_bits).astype(np.float64).reshape(-1)
+    denom = np.abs(r).max()
+    rel = np.abs(g - r).max() / denom if denom > 0 else np.abs(g - r).max()
+    ng, nr = np.linalg.norm(g), np.linalg.norm(r)
+    cos = float(g @ r / (ng * nr)) if ng > 0 and nr > 0 else (1.0 if ng == nr else 0.0)
+    return float(rel), cos
+
+
+REL_TOL = 1e-2
+COS_TOL = 0.9999

@@ -1,0 +1,209 @@
+"""CPU checks of the C-ABI boundary: the four drop-in libraries load, export
+every symbol include/dsv4_kernels.h declares under the reference's file
+names, and return the reference's error codes from host-side validation
+(which runs before any HIP call, so no GPU is needed)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from tests.conftest import PKG, REPO
+
+HEADER = os.path.join(REPO, "include", "dsv4_kernels.h")
+
+LIBS = {
+    "mxfp4-routed/libmxfp4_grouped_gemv.so": [
+        "mxfp4_grouped_gemv_topk", "mxfp4_grouped_workspace_bytes",
+        "mxfp4_moe_route_sigmoid_topk", "mxfp4_moe_workspace_bytes", "mxfp4_moe_grouped_gemv",
+        "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down"],
+    "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
+    "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_dequant_bf16"],
+    "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],
+}
+
+# Symbols the reference engine resolves with dlsym / extern / weak reference
+# (kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4.cu:149-154, routed.cu:46-54, head.cu:302-312).
+REFERENCE_SYMBOLS = ["fp8_e4m3_gemv_m1", "mxfp4_grouped_gemv_topk", "mxfp4_grouped_workspace_bytes",
+                     "rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add", "mxfp4_gemv_m1"]
+
+
+def _lib(rel):
+    path = os.path.join(PKG, "kernel", rel)
+    if not os.path.exists(path):
+        pytest.fail(f"{path} missing: run __graft_entry__.build() first")
+    return ctypes.CDLL(path)
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_exactly_the_exported_set():
+    declared = _declared()
+    exported = sorted(s for syms in LIBS.values() for s in syms)
+    assert declared == exported
+    assert set(REFERENCE_SYMBOLS) <= set(declared)
+
+
+@pytest.mark.parametrize("rel", sorted(LIBS))
+def test_library_exports_symbols(rel):
+    lib = _lib(rel)
+    for sym in LIBS[rel]:
+        assert hasattr(lib, sym), f"{rel} does not export {sym}"
+    out = subprocess.run(["nm", "-D", "--defined-only", os.path.join(PKG, "kernel", rel)],
+                         capture_output=True, text=True, check=True).stdout
+    for sym in LIBS[rel]:
+        assert re.search(rf"\bT {sym}$", out, flags=re.M), f"{sym} not a defined text symbol"
+
+
+def test_header_compiles_as_c():
+    src = f'#include "{HEADER}"\nint main(void) {{ return 0; }}\n'
+    r = subprocess.run(["gcc", "-x", "c", "-std=c99", "-fsyntax-only", "-I/opt/rocm/include",
+                        "-D__HIP_PLATFORM_AMD__", "-"], input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+N = None  # null device pointer: validation returns before any device access
+
+
+def test_grouped_validation_codes():
+    lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
+    f = lib.mxfp4_grouped_gemv_topk
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_int] * 4 + [ctypes.c_void_p] * 3
+
+    def call(K, H, O, n):
+        return f(N, N, N, N, N, N, N, N, K, H, O, n, N, N, N)
+
+    assert call(4095, 2048, 4096, 8) == -1
+    assert call(4096, 2047, 4096, 8) == -2
+    assert call(4128, 2048, 4096, 8) == -3
+    assert call(4096, 4128, 4096, 8) == -3
+    assert call(4096, 2048, 4096, 0) == -4
+    assert call(4096, 2048, 4096, 257) == -4
+    assert call(4096, 2048, 0, 8) == -6
+    ws = lib.mxfp4_grouped_workspace_bytes
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [ctypes.c_int] * 3
+    assert ws(6, 2048, 4096) == 6 * 2048 * 2 + 4096 * 4  # reference formula
+    assert ws(8, 2048, 4096) == 49152
+
+
+def test_moe_validation_codes():
+    lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
+    f = lib.mxfp4_moe_grouped_gemv
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 9 + [ctypes.c_int] * 6 + [ctypes.c_void_p] * 3
+
+    def call(T, k, E, K, H, O):
+        return f(N, N, N, N, N, N, N, N, N, T, k, E, K, H, O, N, N, N)
+
+    assert call(1, 8, 256, 4095, 2048, 4096) == -1
+    assert call(1, 8, 256, 4096, 2047, 4096) == -2
+    assert call(1, 8, 256, 8192, 2048, 4096) == -3
+    assert call(0, 8, 256, 4096, 2048, 4096) == -4
+    assert call(65, 8, 256, 4096, 2048, 4096) == -4
+    assert call(1, 17, 256, 4096, 2048, 4096) == -4
+    assert call(1, 8, 1025, 4096, 2048, 4096) == -4
+    r = lib.mxfp4_moe_route_sigmoid_topk
+    r.restype = ctypes.c_int
+    r.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 3
+    assert r(N, 0, 256, 8, N, N, N) == -1
+    assert r(N, 1, 4, 8, N, N, N) == -1
+    assert r(N, 1, 256, 17, N, N, N) == -1
+    wb = lib.mxfp4_moe_workspace_bytes
+    wb.restype = ctypes.c_size_t
+    wb.argtypes = [ctypes.c_int] * 4
+    assert wb(16, 8, 256, 2048) >= 16 * 8 * 2048 * 2
+    assert wb(0, 8, 256, 2048) == 0
+
+
+def test_dense_validation_codes():
+    lib = _lib("mxfp4-dense/libmxfp4_gemv.so")
+    f = lib.mxfp4_gemv_m1
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p] * 2
+    assert f(N, N, N, 4095, 2048, 2048, 128, N, N) == -1
+    assert f(N, N, N, 8224, 2048, 4112, 257, N, N) == -2
+    assert f(N, N, N, 4096, 0, 2048, 128, N, N) == -3
+    d = lib.mxfp4_dequant_bf16
+    d.restype = ctypes.c_int
+    d.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p] * 2
+    assert d(N, N, 100, 4, 50, 4, N, N) == -1
+
+
+def test_fp8_validation_codes():
+    lib = _lib("fp8-dense/libfp8_e4m3_gemv.so")
+    f = lib.fp8_e4m3_gemv_m1
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 2 + [ctypes.c_int64] * 2 + [ctypes.c_void_p] * 2
+    assert f(N, N, N, 4000, 1536, 4000, 32, N, N) == -1
+    assert f(N, N, N, 16512, 1536, 16512, 129, N, N) == -3
+    assert f(N, N, N, 4096, 0, 4096, 32, N, N) == -4
+    g = lib.fp8_e4m3_gemv
+    g.restype = ctypes.c_int
+    P, I, L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    g.argtypes = [P, L, P, P, I, I, I, L, L, P, L, P]
+    assert g(N, 4096, N, N, 4096, 1536, 0, 4096, 32, N, 1536, N) == -5
+    assert g(N, 4096, N, N, 4096, 1536, 17, 4096, 32, N, 1536, N) == -5
+    assert g(N, 4096, N, N, 4000, 1536, 2, 4096, 32, N, 1536, N) == -1
+
+
+def test_rmsnorm_validation_codes():
+    lib = _lib("rmsnorm-fuse/librmsnorm_fuse.so")
+    f = lib.rmsnorm_fuse_fwd
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 2 + [ctypes.c_float, ctypes.c_void_p]
+    assert f(N, N, N, 0, 4096, 1e-6, N) == 0
+    assert f(N, N, N, 4, 0, 1e-6, N) == 0
+    assert f(N, N, N, 4, 8193, 1e-6, N) == 1
+    g = lib.rmsnorm_fuse_residual_add
+    g.restype = ctypes.c_int
+    g.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 2 + [ctypes.c_float, ctypes.c_void_p]
+    assert g(N, N, N, N, N, -1, 4096, 1e-6, N) == 0
+    assert g(N, N, N, N, N, 4, 8193, 1e-6, N) == 1
+
+
+def test_bindings_import_and_resolve_paths():
+    from runtime import (fp8_e4m3_gemv_binding, mxfp4_gemv_binding, mxfp4_grouped_gemv_binding,
+                         rmsnorm_fuse_binding)
+    for mod, rel in ((mxfp4_grouped_gemv_binding, "mxfp4-routed/libmxfp4_grouped_gemv.so"),
+                     (mxfp4_gemv_binding, "mxfp4-dense/libmxfp4_gemv.so"),
+                     (fp8_e4m3_gemv_binding, "fp8-dense/libfp8_e4m3_gemv.so"),
+                     (rmsnorm_fuse_binding, "rmsnorm-fuse/librmsnorm_fuse.so")):
+        assert mod.lib_path() == os.path.join(PKG, "kernel", rel)
+        mod._load_lib()  # sets argtypes for every exported entry point
+
+
+def test_binding_env_override(monkeypatch, tmp_path):
+    from runtime import mxfp4_gemv_binding
+
+    monkeypatch.setenv("MXFP4_GEMV_LIB", str(tmp_path / "elsewhere.so"))
+    assert mxfp4_gemv_binding.lib_path() == str(tmp_path / "elsewhere.so")
+
+
+def test_bindings_reject_cpu_tensors():
+    import torch
+
+    from runtime import fp8_e4m3_gemv_binding, mxfp4_gemv_binding, mxfp4_grouped_gemv_binding
+    from runtime import rmsnorm_fuse_binding
+
+    x = torch.zeros(4096, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        mxfp4_gemv_binding.mxfp4_gemv(torch.zeros(8, 2048, dtype=torch.uint8),
+                                      torch.zeros(8, 128, dtype=torch.uint8), x)
+    with pytest.raises(RuntimeError):
+        fp8_e4m3_gemv_binding.fp8_e4m3_gemv(torch.zeros(128, 4096, dtype=torch.uint8),
+                                            torch.zeros(1, 32, dtype=torch.uint8), x)
+    w = {"packed": torch.zeros(1, 32, 2048, dtype=torch.uint8),
+         "scale": torch.zeros(1, 32, 128, dtype=torch.uint8)}
+    with pytest.raises(ValueError):
+        mxfp4_grouped_gemv_binding.mxfp4_grouped_gemv(w, w, w, None, x, torch.zeros(1))
+    with pytest.raises(TypeError):
+        rmsnorm_fuse_binding.rmsnorm_fuse_fwd(x.view(1, -1), x)

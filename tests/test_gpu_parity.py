@@ -1,0 +1,316 @@
+"""GPU parity of the four kernels (through the C ABI) against the CPU oracle.
+
+Bar: dequantised weights bit-exact; outputs max rel err <= 1e-2 and cosine
+>= 0.9999 against the oracle's dequant -> fp32 matmul -> bf16 path; integer
+outputs (routing ids, residual sums) bit-exact. Sizes are those of the
+benchmark configurations where the oracle finishes in seconds, smaller ones
+for the exhaustive and edge cases.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mx
+from runtime import fill, synth
+from runtime import fp8_e4m3_gemv_binding as fp8b
+from runtime import mxfp4_gemv_binding as mxb
+from runtime import mxfp4_grouped_gemv_binding as gb
+from runtime import rmsnorm_fuse_binding as rb
+from tests.gpu_util import announce, assert_close, dev_bf16, dev_f32, dev_u8, host_bits
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------ filler --
+
+def test_device_fill_matches_numpy_generator(device):
+    announce("dsv4_fill_uniform_u8 n=1000003 offset=77")
+    t = torch.empty(1000003, dtype=torch.uint8, device=device)
+    fill.fill_uniform_u8(t, 1234, 77)
+    assert np.array_equal(t.cpu().numpy(), synth.uniform_u8(1234, 77, 1000003))
+    s = torch.empty(4099, dtype=torch.uint8, device=device)
+    fill.fill_uniform_u8(s, 99, 5, synth.SCALE_LO, synth.SCALE_HI)
+    assert np.array_equal(s.cpu().numpy(), synth.uniform_u8(99, 5, 4099, 119, 125))
+
+
+# ----------------------------------------------------------------- dequant --
+
+def test_mxfp4_dequant_exhaustive_bit_exact(device):
+    """Every packed byte under every scale byte (0 -> 2^-127, 255 -> 0, 254 -> inf for code 6)."""
+    announce("mxfp4_dequant_bf16 exhaustive 256x512")
+    packed = np.tile(np.arange(256, dtype=np.uint8), (256, 1))
+    scale = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 16, axis=1)
+    got = host_bits(mxb.mxfp4_dequant(dev_u8(packed, device), dev_u8(scale, device)))
+    ref = mx.mxfp4_dequant_bf16(packed, scale, kernel_convention=True)
+    assert np.array_equal(got, ref)
+
+
+def test_mxfp4_dequant_config_weight_bit_exact(device):
+    announce("mxfp4_dequant_bf16 cfg0 2048x4096 seed 1000")
+    p, s = synth.mxfp4_weight(1000, 2048, 4096)
+    got = host_bits(mxb.mxfp4_dequant(dev_u8(p[0], device), dev_u8(s[0], device)))
+    assert np.array_equal(got, mx.mxfp4_dequant_bf16(p[0], s[0]))
+
+
+def test_fp8_dequant_exhaustive_bit_exact(device):
+    """All 256 E4M3FN bytes in every row, a distinct scale byte in each of 256 tiles."""
+    announce("fp8_e4m3_dequant_bf16 exhaustive 2048x2048")
+    w = np.tile(np.arange(256, dtype=np.uint8), (2048, 8))
+    s = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    got = host_bits(fp8b.fp8_e4m3_dequant(dev_u8(w, device), dev_u8(s, device)))
+    ref = mx.fp8_dequant_bf16(w, s, kernel_convention=True)
+    gn = np.isnan(mx.bf16_to_f32(got))
+    rn = np.isnan(mx.bf16_to_f32(ref))
+    assert np.array_equal(gn, rn)
+    assert np.array_equal(got[~gn], ref[~rn])
+
+
+# ------------------------------------------------------------- MXFP4 GEMV --
+
+@pytest.mark.parametrize("N,K", [(2048, 4096), (2047, 4096), (64, 32), (96, 96), (40, 2048),
+                                 (33, 8192), (128, 6144)])
+def test_mxfp4_gemv(device, N, K):
+    announce(f"mxfp4_gemv_m1 N={N} K={K}")
+    p, s = synth.mxfp4_weight(1000 + K, N, K)
+    x = synth.normal_bf16(2000 + K, (K,))
+    y = mxb.mxfp4_gemv(dev_u8(p[0], device), dev_u8(s[0], device), dev_bf16(x, device))
+    assert_close(host_bits(y), mx.mxfp4_gemv(x, p[0], s[0]), f"mxfp4 N={N} K={K}")
+
+
+def test_mxfp4_gemv_row_strides_and_unaligned(device):
+    N, K = 300, 1024
+    p, s = synth.mxfp4_weight(3001, N, K)
+    x = synth.normal_bf16(3002, (K,))
+    ref = mx.mxfp4_gemv(x, p[0], s[0])
+    # rows inside wider buffers (caller strides), 16-byte aligned
+    wide_p = np.zeros((N, K // 2 + 48), np.uint8)
+    wide_p[:, :K // 2] = p[0]
+    wide_s = np.zeros((N, K // 32 + 5), np.uint8)
+    wide_s[:, :K // 32] = s[0]
+    tp, ts = dev_u8(wide_p, device), dev_u8(wide_s, device)
+    announce("mxfp4_gemv_m1 strided rows")
+    y = mxb.mxfp4_gemv(tp[:, :K // 2], ts[:, :K // 32], dev_bf16(x, device))
+    assert_close(host_bits(y), ref, "mxfp4 strided")
+    # unaligned weight rows (offset 1 byte, odd stride) and unaligned activation
+    odd_p = np.zeros((N, K // 2 + 1 + 7), np.uint8)
+    odd_p[:, 1:1 + K // 2] = p[0]
+    to = dev_u8(odd_p, device)
+    xb = dev_bf16(np.concatenate([[0], x]).astype(np.uint16), device)
+    announce("mxfp4_gemv_m1 unaligned rows and activation")
+    y2 = mxb.mxfp4_gemv(to[:, 1:1 + K // 2], ts[:, :K // 32], xb[1:])
+    assert_close(host_bits(y2), ref, "mxfp4 unaligned")
+
+
+def test_mxfp4_gemv_one_hot_selects_column(device):
+    announce("mxfp4_gemv_m1 one-hot 256x512")
+    p, s = synth.mxfp4_weight(3003, 256, 512)
+    deq = mx.bf16_to_f32(mx.mxfp4_dequant_bf16(p[0], s[0]))
+    tp, ts = dev_u8(p[0], device), dev_u8(s[0], device)
+    for k in (0, 33, 511):
+        x = np.zeros(512, np.uint16)
+        x[k] = 0x3F80
+        got = mx.bf16_to_f32(host_bits(mxb.mxfp4_gemv(tp, ts, dev_bf16(x, device))))
+        assert np.array_equal(got, deq[:, k])
+
+
+# --------------------------------------------------------------- FP8 GEMV --
+
+FP8_SHAPES = [(1536, 4096), (576, 4096), (4096, 4096), (4096, 2048)]
+
+
+@pytest.mark.parametrize("N,K", FP8_SHAPES)
+@pytest.mark.parametrize("T", [1, 8])
+def test_fp8_gemv_config_shapes(device, N, K, T):
+    announce(f"fp8_e4m3_gemv N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(1002 + N + K, N, K)
+    x = synth.normal_bf16(2002 + T, (T, K))
+    tw, ts = dev_u8(w, device), dev_u8(s, device)
+    xt = dev_bf16(x, device)
+    y = fp8b.fp8_e4m3_gemv(tw, ts, xt[0] if T == 1 else xt)
+    ref = mx.fp8_gemv(x, w, s)
+    assert_close(host_bits(y).reshape(T, N), ref, f"fp8 N={N} K={K} T={T}")
+
+
+def test_fp8_gemv_long_rows_and_ragged_n(device):
+    N, K, T = 200, 8192, 3
+    announce(f"fp8_e4m3_gemv N={N} K={K} T={T} (two K segments)")
+    w, s = synth.fp8_weight(4001, N, K)
+    x = synth.normal_bf16(4002, (T, K))
+    y = fp8b.fp8_e4m3_gemv(dev_u8(w, device), dev_u8(s, device), dev_bf16(x, device))
+    assert_close(host_bits(y), mx.fp8_gemv(x, w, s), "fp8 K=8192")
+
+
+# ------------------------------------------------------ grouped (drop-in) --
+
+def _packed_experts(seed, n, K, H, O):
+    W1p, W1s = synth.mxfp4_weight(seed, H, K, n)
+    W3p, W3s = synth.mxfp4_weight(seed + 4, H, K, n)
+    W2p, W2s = synth.mxfp4_weight(seed + 8, O, H, n)
+    return W1p, W3p, W2p, W1s, W3s, W2s
+
+
+def _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s):
+    return ({"packed": dev_u8(W1p, device), "scale": dev_u8(W1s, device)},
+            {"packed": dev_u8(W3p, device), "scale": dev_u8(W3s, device)},
+            {"packed": dev_u8(W2p, device), "scale": dev_u8(W2s, device)})
+
+
+@pytest.mark.parametrize("n_exp,K,H,O", [(8, 4096, 2048, 4096), (6, 4096, 2048, 4096),
+                                         (1, 4096, 2048, 4096), (3, 1024, 96, 200)])
+def test_grouped_gemv_topk(device, n_exp, K, H, O):
+    announce(f"mxfp4_grouped_gemv_topk n_exp={n_exp} K={K} H={H} O={O}")
+    mats = _packed_experts(5000 + n_exp, n_exp, K, H, O)
+    x = synth.normal_bf16(5100 + n_exp, (K,))
+    r = synth.normal_f64(5200 + n_exp, 0, n_exp)
+    r = (1 / (1 + np.exp(-r)))
+    r = (r / r.sum()).astype(np.float32)
+    W1, W3, W2 = _dev_mats(device, *mats)
+    out = gb.mxfp4_grouped_gemv(W1, W3, W2, None, dev_bf16(x, device), dev_f32(r, device))
+    ref = mx.grouped_gemv_topk(x, *mats, r)
+    got = host_bits(out)
+    assert_close(got, ref, f"grouped n_exp={n_exp}")
+    # deterministic: a second call is bit-identical
+    out2 = gb.mxfp4_grouped_gemv(W1, W3, W2, None, dev_bf16(x, device), dev_f32(r, device))
+    assert np.array_equal(host_bits(out2), got)
+
+
+def test_grouped_gemv_invariants(device):
+    n, K, H, O = 8, 4096, 2048, 4096
+    mats = _packed_experts(6000, n, K, H, O)
+    x = dev_bf16(synth.normal_bf16(6001, (K,)), device)
+    r = np.linspace(0.05, 0.2, n).astype(np.float32)
+    W1, W3, W2 = _dev_mats(device, *mats)
+    announce("mxfp4_grouped_gemv_topk invariants: zero weights, permutation")
+    zero = gb.mxfp4_grouped_gemv(W1, W3, W2, None, x, torch.zeros(n, device=device))
+    assert np.all(mx.bf16_to_f32(host_bits(zero)) == 0)
+    base = host_bits(gb.mxfp4_grouped_gemv(W1, W3, W2, None, x, dev_f32(r, device)))
+    perm = torch.tensor([3, 7, 0, 5, 1, 6, 2, 4], device=device)
+    Wp = [{k: w[k][perm].contiguous() for k in ("packed", "scale")} for w in (W1, W3, W2)]
+    permuted = host_bits(gb.mxfp4_grouped_gemv(*Wp[:2], Wp[2], None, x,
+                                               dev_f32(r, device)[perm].contiguous()))
+    assert_close(permuted, base, "grouped permuted experts", cos_tol=0.99999)
+
+
+# --------------------------------------------------- expert-indexed MoE -----
+
+def test_route_sigmoid_topk(device):
+    announce("mxfp4_moe_route_sigmoid_topk T=16 E=256 k=8")
+    logits = synth.gating_logits(7001, 16, 256)
+    ids, w = gb.route_sigmoid_topk(dev_f32(logits, device), 8)
+    rids, rw = mx.route_sigmoid_topk(logits, 8)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_moe_indexed_small_dims(device, T):
+    """All T of the config at reduced K/H/O so the oracle covers every expert quickly."""
+    E, K, H, O, topk = 256, 512, 256, 384, 8
+    announce(f"mxfp4_moe_grouped_gemv T={T} E={E} K={K} H={H} O={O}")
+    W1p, W1s = synth.mxfp4_weight(8000, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8004, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8008, O, H, E)
+    x = synth.normal_bf16(8100 + T, (T, K))
+    ids, w = mx.route_sigmoid_topk(synth.gating_logits(8200 + T, T, E), topk)
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    out = gb.mxfp4_moe_grouped_gemv(dev_bf16(x, device), W1, W3, W2,
+                                    torch.from_numpy(ids).to(device), dev_f32(w, device))
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    assert_close(host_bits(out), mx.moe_layer(x, fn, ids, w, O), f"moe T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_indexed_config_dims(device, T):
+    """Config-3 shapes (256 experts, K=4096, H=2048, O=4096) with device-filled weights."""
+    from runtime import moe
+
+    E, K, H, O = 256, 4096, 2048, 4096
+    announce(f"RoutedMoELayer T={T} E={E} (device-filled weights)")
+    weights = moe.make_moe_weights(9000, E, K, H, O, device)
+    layer = moe.RoutedMoELayer(weights, topk=8, max_tokens=16)
+    x = synth.normal_bf16(9100 + T, (T, K))
+    logits = synth.gating_logits(9200 + T, T, E)
+    out = layer.forward(dev_bf16(x, device), logits=dev_f32(logits, device))
+    ids = layer.ids[:T].cpu().numpy()
+    w = layer.weights[:T].cpu().numpy()
+    rids, rw = mx.route_sigmoid_topk(logits, 8)
+    assert np.array_equal(ids, rids)
+
+    def fn(e):
+        # host copy of the device-filled expert (same bytes as the seeded generator)
+        mats = []
+        for m in (weights.W1, weights.W3, weights.W2):
+            mats.append((m["packed"][e].cpu().numpy(), m["scale"][e].cpu().numpy()))
+        return tuple(mats)
+
+    if T == 1:  # the generator regenerates an expert on the host byte for byte
+        e0 = int(ids[0, 0])
+        h = moe.expert_host_weights(9000, e0, K, H, O)
+        d = fn(e0)
+        for (hp, hs), (dp, ds) in zip(h, d):
+            assert np.array_equal(hp, dp) and np.array_equal(hs, ds)
+    assert_close(host_bits(out), mx.moe_layer(x, fn, ids, w, O), f"moe cfg3 T={T}")
+    del layer, weights
+    torch.cuda.empty_cache()
+
+
+def test_moe_indexed_equals_packed_dropin(device):
+    """Full-size T=16: each token's row equals the drop-in call on its packed experts."""
+    from runtime import moe
+
+    E, K, H, O, T = 256, 4096, 2048, 4096, 16
+    announce(f"mxfp4_moe_grouped_gemv vs mxfp4_grouped_gemv_topk T={T}")
+    weights = moe.make_moe_weights(9500, E, K, H, O, device)
+    layer = moe.RoutedMoELayer(weights, topk=8, max_tokens=16)
+    x = dev_bf16(synth.normal_bf16(9600, (T, K)), device)
+    logits = dev_f32(synth.gating_logits(9601, T, E), device)
+    out = host_bits(layer.forward(x, logits=logits))
+    ids = layer.ids[:T].long()
+    for t in range(T):
+        sel = ids[t]
+        W = [{k: m[k][sel].contiguous() for k in ("packed", "scale")}
+             for m in (weights.W1, weights.W3, weights.W2)]
+        ref = host_bits(gb.mxfp4_grouped_gemv(W[0], W[1], W[2], None, x[t].contiguous(),
+                                              layer.weights[t].contiguous()))
+        assert_close(out[t], ref, f"token {t}", cos_tol=0.99999)
+    del layer, weights
+    torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------- RMSNorm ---
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_rmsnorm_residual_config(device, T):
+    H = 4096
+    announce(f"rmsnorm_fuse_residual_add T={T} H={H}")
+    h = synth.normal_bf16(1001 + T, (T, H))
+    r = synth.normal_bf16(1101 + T, (T, H), 0.0, 0.5)
+    g = synth.normal_bf16(1201, (H,), 1.0, 0.1)
+    y, nr = rb.rmsnorm_fuse_residual_add(dev_bf16(h, device), dev_bf16(r, device), dev_bf16(g, device))
+    ry, rnr = mx.rmsnorm_residual(h, r, g)
+    assert np.array_equal(host_bits(nr), rnr)  # single RNE rounding of an exact sum
+    assert_close(host_bits(y), ry, f"rmsnorm residual T={T}")
+    announce(f"rmsnorm_fuse_fwd T={T} H={H}")
+    y2 = rb.rmsnorm_fuse_fwd(dev_bf16(h, device), dev_bf16(g, device))
+    assert_close(host_bits(y2), mx.rmsnorm(h, g), f"rmsnorm fwd T={T}")
+
+
+def test_rmsnorm_scalar_path_and_noop(device):
+    H, T = 4001, 3  # H % 8 != 0 -> scalar kernel
+    announce(f"rmsnorm_fuse_residual_add scalar path T={T} H={H}")
+    h = synth.normal_bf16(1301, (T, H))
+    r = synth.normal_bf16(1302, (T, H), 0.0, 0.5)
+    g = synth.normal_bf16(1303, (H,), 1.0, 0.1)
+    y, nr = rb.rmsnorm_fuse_residual_add(dev_bf16(h, device), dev_bf16(r, device), dev_bf16(g, device))
+    ry, rnr = mx.rmsnorm_residual(h, r, g)
+    assert np.array_equal(host_bits(nr), rnr)
+    assert_close(host_bits(y), ry, "rmsnorm scalar")
+    c = dev_bf16(np.full((2, 64), 0x3F40, np.uint16), device)  # constant rows 0.75
+    gw = dev_bf16(np.full(64, 0x3F80, np.uint16), device)
+    yc = mx.bf16_to_f32(host_bits(rb.rmsnorm_fuse_fwd(c, gw)))
+    assert np.allclose(yc, 0.75 / np.sqrt(0.75 ** 2 + 1e-6), rtol=4e-3)
