@@ -1,11 +1,13 @@
 #!/usr/bin/env python3
 """bench.py — routed-MoE decode layer on one MI355X.
 
-One step = one routed-MoE layer at decode: device gating of N(0,1) logits over
-256 experts (top-8, sigmoid weights renormalised), then the expert-indexed
-MXFP4 grouped GEMV (routing tables, stage A = W1/W3 + SiLU, stage B = W2 +
-weighted combine) reading the routed experts in place from HBM-resident
-per-layer tensors. Inputs are resident in HBM before the timed region. Steps
+One step = one routed-MoE layer at decode (mxfp4_moe_layer, three kernels):
+device gating of N(0,1) logits over 256 experts (top-8, sigmoid weights
+renormalised) fused with the routing tables, then stage A (W1/W3 + SiLU) and
+stage B (W2 + weighted combine) of the expert-indexed MXFP4 grouped GEMV,
+reading the routed experts in place from HBM-resident per-layer tensors. The
+K timed steps are captured once in a HIP graph and replayed (the eager,
+host-issued timing of the same steps is reported beside it). Inputs are resident in HBM before the timed region. Steps
 cycle over --layers layers of 256 experts (4 x 3.42 GB by default) with fresh
 logits each step, so weights come from HBM, not the 256 MB MALL.
 
@@ -90,7 +92,7 @@ def main() -> int:
 
     log(f"allocating {L} layers x {E} experts ({L * E * EXPERT_BYTES / 1e9:.2f} GB)")
     layers = [moe.make_moe_weights(20000 + 100 * l, E, K, H, O, dev) for l in range(L)]
-    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=max(16, T)) for w in layers]
+    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=max(16, T), check=False) for w in layers]
     x = torch.from_numpy(synth.normal_bf16(3001, (T, K)).view(np.int16)).view(torch.bfloat16).to(dev)
     logits_h = synth.gating_logits(3002, n_steps * T, E).reshape(n_steps, T, E)
     logits = torch.from_numpy(logits_h).to(dev)
@@ -102,18 +104,40 @@ def main() -> int:
     def step(i: int):
         return mods[i % L].forward(x, logits=logits[i])
 
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn) -> float:
+        torch.cuda.synchronize()
+        ev0.record()
+        fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1)
+
     log(f"warmup {args.warmup} steps, T={T}")
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    log(f"timing {args.steps} steps")
-    ev0.record()
-    for i in range(args.warmup, n_steps):
-        step(i)
-    ev1.record()
+
+    # The K timed steps, captured once as a HIP graph (3 kernels per step, no
+    # memsets) and replayed: the device-side cost of a decode loop whose host
+    # issues one graph launch. The same K steps issued eagerly are timed too.
+    log(f"capturing {args.steps} steps in a HIP graph")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(args.warmup, n_steps):
+            step(i)
+    graph.replay()
     torch.cuda.synchronize()
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    log(f"timing {args.steps} steps (graph replay)")
+    ms_per_step = timed(graph.replay) / args.steps
+    log(f"timing {args.steps} steps (eager)")
+
+    def eager():
+        for i in range(args.warmup, n_steps):
+            step(i)
+
+    ms_per_step_eager = timed(eager) / args.steps
     timed_bytes = float(step_bytes[args.warmup:].mean())
     value = timed_bytes / (ms_per_step * 1e-3) / 1e9
 
@@ -130,25 +154,23 @@ def main() -> int:
         st.swiglu(x)
         st.down(out)
     torch.cuda.synchronize()
-    reps = max(1, args.steps // R)
-    log(f"timing stage A alone: {reps * R} launches")
-    ev0.record()
-    for _ in range(reps):
+    ga, gbr = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ga):
         for st in stages:
             st.swiglu(x)
-    ev1.record()
-    torch.cuda.synchronize()
-    a_us = ev0.elapsed_time(ev1) * 1e3 / (reps * R)
-    ev0.record()
-    for _ in range(reps):
+    with torch.cuda.graph(gbr):
         for st in stages:
             st.down(out)
-    ev1.record()
-    torch.cuda.synchronize()
-    b_us = ev0.elapsed_time(ev1) * 1e3 / (reps * R)
+    ga.replay()
+    gbr.replay()
+    reps = max(1, args.steps // R)
+    log(f"timing stage A alone: {reps * R} launches (graph)")
+    a_us = timed(lambda: [ga.replay() for _ in range(reps)]) * 1e3 / (reps * R)
+    b_us = timed(lambda: [gbr.replay() for _ in range(reps)]) * 1e3 / (reps * R)
     a_bytes = float(np.mean(uniq[:R] * STAGE_A_EXPERT_BYTES + T * K * 2 + T * TOPK * H * 2))
     b_bytes = float(np.mean(uniq[:R] * STAGE_B_EXPERT_BYTES + T * TOPK * H * 2 + T * O * 2))
     a_gbs = a_bytes / (a_us * 1e-6) / 1e9
+    b_gbs = b_bytes / (b_us * 1e-6) / 1e9
 
     # --- CPU baseline: the oracle (dequant + fp32 matmul) on step 0's experts ---
     cpu = None
@@ -217,8 +239,10 @@ def main() -> int:
             "algorithmic_bytes_per_step": int(round(timed_bytes)),
         },
         "moe_layer_us": round(ms_per_step * 1e3, 3),
+        "moe_layer_us_eager": round(ms_per_step_eager * 1e3, 3),
         "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         "stage_us": {"swiglu_A": round(a_us, 3), "down_B": round(b_us, 3)},
+        "stage_gbs": {"swiglu_A": round(a_gbs, 1), "down_B": round(b_gbs, 1)},
         "roofline": {
             "kernel": "moe_swiglu_kernel (stage A: W1+W3 MXFP4 GEMV + SiLU)",
             "bound": "hbm",

@@ -101,6 +101,20 @@ __device__ __forceinline__ float fp8_chunk_dot(const u32x4 w, const uint32_t* xp
     return a0 + a1;
 }
 
+// Marks a register value as modified (emits no instruction). Used inside
+// loops whose weights stay in registers across iterations, so the compiler
+// cannot hoist the per-iteration decode out of the loop and keep every decoded
+// value live at once (which multiplies the register footprint).
+__device__ __forceinline__ void reg_barrier(u32x4& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void reg_barrier(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
+// As reg_barrier, and additionally orders the decode of `v` after `dep` is
+// computed: chaining blocks this way keeps one block's decoded values live at
+// a time instead of letting the compiler decode every block up front.
+__device__ __forceinline__ void reg_barrier_after(u32x4& v, float dep) {
+    asm volatile("" : "+v"(v) : "v"(dep));
+}
+
 // ---------------------------------------------------------------- loads ----
 
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
@@ -130,10 +144,47 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Value held by the partner lane in a butterfly step over lane bit MASK.
+// Partners differ in that bit (and, for 4 and 8, in lower bits too, via the
+// mirror patterns); every pattern is an involution, which is all a butterfly
+// needs. Bits 0-3 use DPP (quad_perm, row_half_mirror, row_mirror); bits 4
+// and 5 use v_permlane16_swap / v_permlane32_swap, whose two results hold the
+// own and the partner value, told apart by comparison with the own value.
+template <int MASK>
+__device__ __forceinline__ uint32_t wave_partner(uint32_t v) {
+    if constexpr (MASK == 1) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (MASK == 2) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (MASK == 4) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false);
+    else if constexpr (MASK == 8) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false);
+    else if constexpr (MASK == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return r[0] == v ? r[1] : r[0];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return r[0] == v ? r[1] : r[0];
+    }
+}
+
+__device__ __forceinline__ float partner_add(float keep, float send, int mask) {
+    const uint32_t s = __float_as_uint(send);
+    uint32_t o;
+    switch (mask) {
+        case 32: o = wave_partner<32>(s); break;
+        case 16: o = wave_partner<16>(s); break;
+        case 8: o = wave_partner<8>(s); break;
+        case 4: o = wave_partner<4>(s); break;
+        case 2: o = wave_partner<2>(s); break;
+        default: o = wave_partner<1>(s); break;
+    }
+    return keep + __uint_as_float(o);
+}
+
 // Butterfly reduction of N values per lane over the 64 lanes of a wave
-// (N a power of two, N <= 64). Each exchange step halves the number of live
-// values, so N sums cost about N + 5 shuffles instead of 6N. On return every
-// lane holds in v[0] the wave total of value index (lane >> (6 - log2 N)).
+// (N a power of two, N <= 64), on the DPP / permlane paths. Each exchange step
+// halves the number of live values, so N sums cost about N + 5 exchanges
+// instead of 6N. On return every lane holds in v[0] the wave total of value
+// index (lane >> (6 - log2 N)). Masks go 32, 16, ..., 1; the partner of a lane
+// at mask m always has the opposite bit m, so "upper" is well defined.
 template <int N>
 struct WaveButterfly {
     static __device__ __forceinline__ void run(float* v, int lane, int mask) {
@@ -143,7 +194,7 @@ struct WaveButterfly {
         for (int i = 0; i < H; ++i) {
             const float send = upper ? v[i] : v[i + H];
             const float keep = upper ? v[i + H] : v[i];
-            v[i] = keep + __shfl_xor(send, mask, kWave);
+            v[i] = partner_add(keep, send, mask);
         }
         WaveButterfly<H>::run(v, lane, mask >> 1);
     }
@@ -152,13 +203,59 @@ template <>
 struct WaveButterfly<1> {
     static __device__ __forceinline__ void run(float* v, int, int mask) {
 #pragma unroll
-        for (; mask > 0; mask >>= 1) v[0] += __shfl_xor(v[0], mask, kWave);
+        for (; mask > 0; mask >>= 1) v[0] = partner_add(v[0], v[0], mask);
     }
 };
 
 template <int N>
 __device__ __forceinline__ void wave_reduce_n(float* v, int lane) {
     WaveButterfly<N>::run(v, lane, 32);
+}
+
+// Whole-wave reductions on the DPP / permlane paths (no LDS traffic):
+// xor 1 and xor 2 via quad_perm, then row_half_mirror and row_mirror (which
+// pair every lane with one in the other half of its 8- and 16-lane group),
+// then v_permlane16_swap / v_permlane32_swap across rows and wave halves.
+// Every lane ends with the result.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_allreduce_u32(uint32_t v, Op op) {
+    v = op(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_u32<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_u32<0x140>(v));  // row_mirror
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = op(r[0], r[1]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = op(r[0], r[1]);
+    }
+    return v;
+}
+
+// Maximum over the wave; NaN inputs are ignored (IEEE maxNum).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    return __uint_as_float(wave_allreduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+    return (int)wave_allreduce_u32((uint32_t)v, [](uint32_t a, uint32_t b) {
+        return (uint32_t)min((int)a, (int)b);
+    });
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    return __uint_as_float(wave_allreduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+    }));
 }
 
 template <int N>

@@ -50,9 +50,6 @@ constexpr int kMaxTopk = 16;
 constexpr int kMaxExperts = 1024;
 
 constexpr int kWavesA = 4;              // waves per stage-A workgroup
-constexpr int kHpw = 4;                 // hidden rows (of W1 and W3) per wave pass
-constexpr int kRowsB = 8;               // output rows per stage-B workgroup
-constexpr int kWavesB = 4;              // waves per stage-B workgroup
 
 // ------------------------------------------------------------ routing set --
 
@@ -125,6 +122,29 @@ __device__ __forceinline__ void load_act_block(const uint16_t* src, uint32_t* xp
     }
 }
 
+// NB consecutive E8M0 bytes of a lane's blocks, packed little-endian; bytes of
+// blocks at or past nblk read as 0 (their weights are zero-filled too).
+template <int NB>
+__device__ __forceinline__ uint32_t load_scales(const uint8_t* p, bool vec_ok, int avail) {
+    if constexpr (NB == 1) {
+        return avail > 0 ? (uint32_t)p[0] : 0u;
+    } else {
+        if (vec_ok) {
+            if constexpr (NB == 2) return *reinterpret_cast<const uint16_t*>(p);
+            else return *reinterpret_cast<const uint32_t*>(p);
+        }
+        uint32_t v = 0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            if (j < avail) v |= (uint32_t)p[j] << (8 * j);
+        return v;
+    }
+}
+
+__device__ __forceinline__ float scale_of(uint32_t packed, int j) {
+    return e8m0_to_f32((packed >> (8 * j)) & 0xFFu);
+}
+
 // ---------------------------------------------------------------- stage A --
 
 struct StageAArgs {
@@ -137,14 +157,32 @@ struct StageAArgs {
     int64_t s_exp_stride;       // bytes per expert: hidden * K/32
     int K;
     int hidden;
-    int h_per_wave;             // multiple of kHpw
+    int h_per_wave;             // multiple of the chunk height
+    int scale_vec;              // scale rows allow NB-byte vector loads
     uint16_t* M;                // [pairs, hidden] bf16
     ExpertSet es;
 };
 
+// HC hidden rows of W1 and of W3 in registers: NB 16-byte blocks per lane per
+// row (lane l owns blocks NB*l .. NB*l+NB-1, so its activation slice and its
+// scale bytes are contiguous) plus the rows' packed scale bytes.
+template <int NB, int HC>
+struct GateUpChunk {
+    u32x4 w1[HC][NB];
+    u32x4 w3[HC][NB];
+    uint32_t s1[HC];
+    uint32_t s3[HC];
+};
+
 // grid = (ceil(hidden / (kWavesA*h_per_wave)), expert slots), block = 64*kWavesA.
-template <int NB, bool INDEXED, bool ALIGNED>
-__global__ __launch_bounds__(64 * kWavesA) void moe_swiglu_kernel(const StageAArgs a) {
+// Each wave walks its hidden rows in chunks of HC with two register buffers:
+// the loads of chunk c+1 are in flight while chunk c is reduced. On the FAST
+// path every load is unconditional (a prefetch past the wave's last chunk
+// re-reads the current one, which hits in cache), so the compiler can wait on
+// exactly the loads a chunk needs rather than draining the prefetch.
+template <int NB, int HC, bool INDEXED, bool FAST, bool PIPE, bool MULTI>
+__global__ __launch_bounds__(64 * kWavesA, PIPE ? 1 : 4) void moe_swiglu_kernel(const StageAArgs a) {
+    constexpr bool ALIGNED = FAST;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     int expert, pbeg, pend;
@@ -156,81 +194,231 @@ __global__ __launch_bounds__(64 * kWavesA) void moe_swiglu_kernel(const StageAAr
     const int K = a.K;
     const int nblk = K / kBlkElems;
     const int64_t wrow = K / 2;
+    const int b0 = NB * lane;
+    const int avail = nblk - b0;  // blocks of this lane inside the row (may be <= 0)
     const uint8_t* W1 = a.w1 + (int64_t)expert * a.w_exp_stride;
     const uint8_t* W3 = a.w3 + (int64_t)expert * a.w_exp_stride;
     const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride;
     const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride;
 
-    bool bvalid[NB];
+    // Rows h0 .. h0+HC-1; on the FAST path rows past h_end are clamped to the
+    // last row (loaded, never stored).
+    auto load_chunk = [&](int h0, GateUpChunk<NB, HC>& c) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) bvalid[j] = (lane + 64 * j) < nblk;
+        for (int r = 0; r < HC; ++r) {
+            if constexpr (FAST) {
+                const int h = min(h0 + r, h_end - 1);
+                const int64_t so = (int64_t)h * nblk + b0;
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const int64_t wo = (int64_t)h * wrow + (int64_t)(b0 + j) * 16;
+                    c.w1[r][j] = ld16_stream(W1 + wo);
+                    c.w3[r][j] = ld16_stream(W3 + wo);
+                }
+                c.s1[r] = load_scales<NB>(S1 + so, true, NB);
+                c.s3[r] = load_scales<NB>(S3 + so, true, NB);
+            } else {
+                const int h = h0 + r;
+                const bool hv = h < h_end;
+                const int64_t so = (int64_t)h * nblk + b0;
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    if (hv && j < avail) {
+                        const int64_t wo = (int64_t)h * wrow + (int64_t)(b0 + j) * 16;
+                        c.w1[r][j] = load_w16<ALIGNED>(W1 + wo);
+                        c.w3[r][j] = load_w16<ALIGNED>(W3 + wo);
+                    } else {
+                        c.w1[r][j] = u32x4{0u, 0u, 0u, 0u};
+                        c.w3[r][j] = u32x4{0u, 0u, 0u, 0u};
+                    }
+                }
+                c.s1[r] = hv ? load_scales<NB>(S1 + so, a.scale_vec, avail) : 0u;
+                c.s3[r] = hv ? load_scales<NB>(S3 + so, a.scale_vec, avail) : 0u;
+            }
+        }
+    };
 
     uint32_t xs[NB][16];
     auto load_x = [&](int tok) {
         const uint16_t* xt = a.x + (int64_t)tok * K;
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if (bvalid[j]) {
-                load_act_block<ALIGNED>(xt + (lane + 64 * j) * kBlkElems, xs[j]);
+            if (FAST || j < avail) {
+                load_act_block<ALIGNED>(xt + (b0 + j) * kBlkElems, xs[j]);
             } else {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) xs[j][q] = 0u;
             }
         }
     };
-    if constexpr (!INDEXED) load_x(0);
 
-    for (int h0 = h_begin; h0 < h_end; h0 += kHpw) {
-        u32x4 w1v[kHpw][NB], w3v[kHpw][NB];
-        uint32_t s1v[kHpw][NB], s3v[kHpw][NB];
+    // Dot products of one chunk against xs, reduced over the wave, SwiGLU'd
+    // and stored as bf16 M[p, h0 + r] by one lane per row.
+    auto emit = [&](GateUpChunk<NB, HC>& c, int h0, int p) {
+        float g[HC], u[HC];
+        float chain = 0.f;
 #pragma unroll
-        for (int r = 0; r < kHpw; ++r) {
-            const int h = h0 + r;
+        for (int r = 0; r < HC; ++r) {
+            float gg = 0.f, uu = 0.f;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
-                const int b = lane + 64 * j;
-                if (h < h_end && bvalid[j]) {
-                    const int64_t wo = (int64_t)h * wrow + (int64_t)b * 16;
-                    const int64_t so = (int64_t)h * nblk + b;
-                    w1v[r][j] = load_w16<ALIGNED>(W1 + wo);
-                    w3v[r][j] = load_w16<ALIGNED>(W3 + wo);
-                    s1v[r][j] = S1[so];
-                    s3v[r][j] = S3[so];
-                } else {
-                    w1v[r][j] = u32x4{0u, 0u, 0u, 0u};
-                    w3v[r][j] = u32x4{0u, 0u, 0u, 0u};
-                    s1v[r][j] = 0u;
-                    s3v[r][j] = 0u;
-                }
+                reg_barrier_after(c.w1[r][j], chain);
+                gg = fmaf(fp4_block_dot(c.w1[r][j], xs[j]), scale_of(c.s1[r], j), gg);
+                reg_barrier_after(c.w3[r][j], gg);
+                uu = fmaf(fp4_block_dot(c.w3[r][j], xs[j]), scale_of(c.s3[r], j), uu);
+                chain = uu;
             }
+            g[r] = gg;
+            u[r] = uu;
         }
-        for (int p = pbeg; p < pend; ++p) {
-            if constexpr (INDEXED) {
+        wave_reduce_n<HC>(g, lane);
+        wave_reduce_n<HC>(u, lane);
+        const int r = reduced_index<HC>(lane);
+        if (reduced_owner<HC>(lane) && h0 + r < h_end)
+            a.M[(int64_t)p * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
+    };
+
+    GateUpChunk<NB, HC> ca, cb;
+    if (!MULTI || pend - pbeg == 1) {
+        // One (token, weight) pair: the activation stays in registers and the
+        // chunks stream through a two-deep pipeline.
+        int tok;
+        float wt;
+        pair_info<INDEXED>(a.es, pbeg, tok, wt);
+        load_x(tok);
+        load_chunk(h_begin, ca);
+        if constexpr (!PIPE) {
+            // One chunk per wave (h_per_wave == HC): occupancy, not a loop,
+            // overlaps the loads of different waves.
+            emit(ca, h_begin, pbeg);
+            return;
+        }
+        int h0 = h_begin;
+        while (true) {
+            const int hn = h0 + HC < h_end ? h0 + HC : h0;
+            if constexpr (FAST) load_chunk(hn, cb);
+            else if (hn != h0) load_chunk(hn, cb);
+            emit(ca, h0, pbeg);
+            h0 += HC;
+            if (h0 >= h_end) break;
+            const int hm = h0 + HC < h_end ? h0 + HC : h0;
+            if constexpr (FAST) load_chunk(hm, ca);
+            else if (hm != h0) load_chunk(hm, ca);
+            emit(cb, h0, pbeg);
+            h0 += HC;
+            if (h0 >= h_end) break;
+        }
+    } else if constexpr (MULTI) {
+        // Several tokens share this expert: each chunk is loaded once and
+        // reduced against every token's activation.
+#pragma unroll 1
+        for (int h0 = h_begin; h0 < h_end; h0 += HC) {
+            load_chunk(h0, ca);
+#pragma unroll 1
+            for (int p = pbeg; p < pend; ++p) {
                 int tok;
                 float wt;
                 pair_info<INDEXED>(a.es, p, tok, wt);
                 load_x(tok);
-            }
-            float g[kHpw], u[kHpw];
 #pragma unroll
-            for (int r = 0; r < kHpw; ++r) {
-                float gg = 0.f, uu = 0.f;
+                for (int r = 0; r < HC; ++r) {
 #pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    gg = fmaf(fp4_block_dot(w1v[r][j], xs[j]), e8m0_to_f32(s1v[r][j]), gg);
-                    uu = fmaf(fp4_block_dot(w3v[r][j], xs[j]), e8m0_to_f32(s3v[r][j]), uu);
+                    for (int j = 0; j < NB; ++j) {
+                        reg_barrier(ca.w1[r][j]);
+                        reg_barrier(ca.w3[r][j]);
+                    }
                 }
-                g[r] = gg;
-                u[r] = uu;
-            }
-            wave_reduce_n<kHpw>(g, lane);
-            wave_reduce_n<kHpw>(u, lane);
-            const int r = reduced_index<kHpw>(lane);
-            if (reduced_owner<kHpw>(lane) && h0 + r < h_end) {
-                a.M[(int64_t)p * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
+                emit(ca, h0, p);
             }
         }
     }
+}
+
+// One token (T = 1, or the drop-in entry) on the FAST path: a workgroup of
+// kT1Waves waves covers kT1Waves*HC hidden rows of one routed expert. The
+// workgroup stages the token's activation in LDS once (one 16-byte load per
+// thread; before or after the weight loads are issued, XFIRST) and every lane
+// copies its slice into registers, so the activation costs one L2 read per
+// workgroup instead of one per wave. Rows past `hidden` are clamped (loaded,
+// not stored) so every wave reaches the barrier.
+template <int NB, int HC, bool INDEXED, int kT1Waves, bool XFIRST>
+__global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const StageAArgs a) {
+    __shared__ u32x4 xl[kMaxRed * 2 / 16];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int expert, pbeg, pend;
+    if (!slot_info<INDEXED>(a.es, blockIdx.y, expert, pbeg, pend)) return;  // whole workgroup
+    const int h0 = (blockIdx.x * kT1Waves + wave) * HC;
+    const int K = a.K;
+    const int nblk = K / kBlkElems;
+    const int64_t wrow = K / 2;
+    const int b0 = NB * lane;
+    const uint8_t* W1 = a.w1 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* W3 = a.w3 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride;
+    const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride;
+
+    int tok;
+    float wt;
+    pair_info<INDEXED>(a.es, pbeg, tok, wt);
+    const u32x4* xg = reinterpret_cast<const u32x4*>(a.x + (int64_t)tok * K);
+    if constexpr (XFIRST) {
+        for (int i = threadIdx.x; i < K / 8; i += 64 * kT1Waves) xl[i] = xg[i];
+        __syncthreads();
+    }
+    GateUpChunk<NB, HC> c;
+#pragma unroll
+    for (int r = 0; r < HC; ++r) {
+        const int h = min(h0 + r, a.hidden - 1);
+        const int64_t so = (int64_t)h * nblk + b0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int64_t wo = (int64_t)h * wrow + (int64_t)(b0 + j) * 16;
+            c.w1[r][j] = ld16_stream(W1 + wo);
+            c.w3[r][j] = ld16_stream(W3 + wo);
+        }
+        c.s1[r] = load_scales<NB>(S1 + so, true, NB);
+        c.s3[r] = load_scales<NB>(S3 + so, true, NB);
+    }
+
+    if constexpr (!XFIRST) {
+        for (int i = threadIdx.x; i < K / 8; i += 64 * kT1Waves) xl[i] = xg[i];
+        __syncthreads();
+    }
+    uint32_t xs[NB][16];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = xl[(b0 + j) * 4 + q];
+            xs[j][4 * q + 0] = v[0];
+            xs[j][4 * q + 1] = v[1];
+            xs[j][4 * q + 2] = v[2];
+            xs[j][4 * q + 3] = v[3];
+        }
+    }
+
+    float g[HC], u[HC];
+    float chain = 0.f;
+#pragma unroll
+    for (int r = 0; r < HC; ++r) {
+        float gg = 0.f, uu = 0.f;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            reg_barrier_after(c.w1[r][j], chain);
+            gg = fmaf(fp4_block_dot(c.w1[r][j], xs[j]), scale_of(c.s1[r], j), gg);
+            reg_barrier_after(c.w3[r][j], gg);
+            uu = fmaf(fp4_block_dot(c.w3[r][j], xs[j]), scale_of(c.s3[r], j), uu);
+            chain = uu;
+        }
+        g[r] = gg;
+        u[r] = uu;
+    }
+    wave_reduce_n<HC>(g, lane);
+    wave_reduce_n<HC>(u, lane);
+    const int r = reduced_index<HC>(lane);
+    if (reduced_owner<HC>(lane) && h0 + r < a.hidden)
+        a.M[(int64_t)pbeg * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
 }
 
 // ---------------------------------------------------------------- stage B --
@@ -244,14 +432,28 @@ struct StageBArgs {
     int hidden;
     int out_dim;
     int T;
+    int scale_vec;
     uint16_t* out;              // [T, out_dim] bf16
     ExpertSet es;
 };
 
-// grid = ceil(out_dim / kRowsB), block = 64*kWavesB. Waves take expert slots
-// wave, wave+kWavesB, ...; partial sums per (wave, token, row) meet in LDS.
-template <int NBB, int TMAX, bool INDEXED, bool ALIGNED>
-__global__ __launch_bounds__(64 * kWavesB) void moe_down_kernel(const StageBArgs a) {
+template <int NBB, int RB>
+struct DownRows {
+    u32x4 w[RB][NBB];
+    uint32_t s[RB];
+};
+
+// grid = ceil(out_dim / kRowsB), block = 64*kWavesB. Wave w takes expert
+// slots w, w+kWavesB, ... for the workgroup's kRowsB output rows, with the
+// next slot's rows loading while the current one is reduced (on the FAST path
+// the prefetch is unconditional: past the last slot it re-reads the current
+// rows); partial sums per (wave, token, row) meet in LDS and are added in wave
+// order.
+template <int NBB, int RB, int WB, int TMAX, bool INDEXED, bool FAST, bool PIPE, bool MULTI>
+__global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_down_kernel(const StageBArgs a) {
+    constexpr bool ALIGNED = FAST;
+    constexpr int kRowsB = RB;
+    constexpr int kWavesB = WB;
     __shared__ float acc[kWavesB][TMAX][kRowsB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -265,59 +467,104 @@ __global__ __launch_bounds__(64 * kWavesB) void moe_down_kernel(const StageBArgs
     else U = a.es.n_slots;
     const int nblk = a.hidden / kBlkElems;
     const int64_t wrow = a.hidden / 2;
-    bool bvalid[NBB];
-#pragma unroll
-    for (int j = 0; j < NBB; ++j) bvalid[j] = (lane + 64 * j) < nblk;
+    const int b0 = NBB * lane;
+    const int avail = nblk - b0;
 
-    for (int u = wave; u < U; u += kWavesB) {
+    auto load_rows = [&](int u, DownRows<NBB, RB>& d) {
         int expert, pbeg, pend;
         slot_info<INDEXED>(a.es, u, expert, pbeg, pend);
         const uint8_t* W2 = a.w2 + (int64_t)expert * a.w_exp_stride;
         const uint8_t* S2 = a.s2 + (int64_t)expert * a.s_exp_stride;
-        u32x4 wv[kRowsB][NBB];
-        uint32_t sv[kRowsB][NBB];
 #pragma unroll
         for (int r = 0; r < kRowsB; ++r) {
-            const int o = o0 + r;
+            if constexpr (FAST) {
+                const int o = min(o0 + r, a.out_dim - 1);
 #pragma unroll
-            for (int j = 0; j < NBB; ++j) {
-                const int b = lane + 64 * j;
-                if (o < a.out_dim && bvalid[j]) {
-                    wv[r][j] = load_w16<ALIGNED>(W2 + (int64_t)o * wrow + (int64_t)b * 16);
-                    sv[r][j] = S2[(int64_t)o * nblk + b];
-                } else {
-                    wv[r][j] = u32x4{0u, 0u, 0u, 0u};
-                    sv[r][j] = 0u;
+                for (int j = 0; j < NBB; ++j)
+                    d.w[r][j] = ld16_stream(W2 + (int64_t)o * wrow + (int64_t)(b0 + j) * 16);
+                d.s[r] = load_scales<NBB>(S2 + (int64_t)o * nblk + b0, true, NBB);
+            } else {
+                const int o = o0 + r;
+                const bool ov = o < a.out_dim;
+#pragma unroll
+                for (int j = 0; j < NBB; ++j) {
+                    if (ov && j < avail)
+                        d.w[r][j] = load_w16<ALIGNED>(W2 + (int64_t)o * wrow + (int64_t)(b0 + j) * 16);
+                    else
+                        d.w[r][j] = u32x4{0u, 0u, 0u, 0u};
                 }
+                d.s[r] = ov ? load_scales<NBB>(S2 + (int64_t)o * nblk + b0, a.scale_vec, avail) : 0u;
             }
         }
+    };
+    auto process = [&](DownRows<NBB, RB>& d, int u) {
+        int expert, pbeg, pend;
+        slot_info<INDEXED>(a.es, u, expert, pbeg, pend);
+        if constexpr (!MULTI) pend = pbeg + 1;  // one pair per slot (T == 1)
+#pragma unroll 1
         for (int p = pbeg; p < pend; ++p) {
             int tok;
             float wt;
             pair_info<INDEXED>(a.es, p, tok, wt);
+            if (MULTI && pend - pbeg > 1) {
+#pragma unroll
+                for (int r = 0; r < kRowsB; ++r) {
+#pragma unroll
+                    for (int j = 0; j < NBB; ++j) reg_barrier(d.w[r][j]);
+                }
+            }
             uint32_t ms[NBB][16];
 #pragma unroll
             for (int j = 0; j < NBB; ++j) {
-                if (bvalid[j]) {
-                    load_act_block<true>(a.M + (int64_t)p * a.hidden + (lane + 64 * j) * kBlkElems,
-                                         ms[j]);
+                if (FAST || j < avail) {
+                    load_act_block<true>(a.M + (int64_t)p * a.hidden + (b0 + j) * kBlkElems, ms[j]);
                 } else {
 #pragma unroll
                     for (int q = 0; q < 16; ++q) ms[j][q] = 0u;
                 }
             }
             float part[kRowsB];
+            float chain = 0.f;
 #pragma unroll
             for (int r = 0; r < kRowsB; ++r) {
                 float s = 0.f;
 #pragma unroll
-                for (int j = 0; j < NBB; ++j)
-                    s = fmaf(fp4_block_dot(wv[r][j], ms[j]), e8m0_to_f32(sv[r][j]), s);
+                for (int j = 0; j < NBB; ++j) {
+                    reg_barrier_after(d.w[r][j], chain);
+                    s = fmaf(fp4_block_dot(d.w[r][j], ms[j]), scale_of(d.s[r], j), s);
+                    chain = s;
+                }
                 part[r] = s;
             }
             wave_reduce_n<kRowsB>(part, lane);
             const int r = reduced_index<kRowsB>(lane);
-            if (reduced_owner<kRowsB>(lane)) acc[wave][tok][r] += wt * part[0];
+            if (reduced_owner<kRowsB>(lane) && o0 + r < a.out_dim) acc[wave][tok][r] += wt * part[0];
+        }
+    };
+
+    DownRows<NBB, RB> da, db;
+    int u = wave;
+    if (!PIPE) {
+#pragma unroll 1
+        for (; u < U; u += kWavesB) {
+            load_rows(u, da);
+            process(da, u);
+        }
+    } else if (u < U) {
+        load_rows(u, da);
+        while (true) {
+            const int un = u + kWavesB < U ? u + kWavesB : u;
+            if constexpr (FAST) load_rows(un, db);
+            else if (un != u) load_rows(un, db);
+            process(da, u);
+            u += kWavesB;
+            if (u >= U) break;
+            const int um = u + kWavesB < U ? u + kWavesB : u;
+            if constexpr (FAST) load_rows(um, da);
+            else if (um != u) load_rows(um, da);
+            process(db, u);
+            u += kWavesB;
+            if (u >= U) break;
         }
     }
     __syncthreads();
@@ -345,114 +592,198 @@ struct RouteTables {
     float* pair_w;              // [T*topk] routing weight of each pair
 };
 
-// One workgroup of 1024 threads: histogram of expert ids, one scan giving each
-// routed expert its slot and pair offset, then each routed expert lists its
-// (token, weight) pairs in token order. Deterministic for any input order.
-__global__ __launch_bounds__(1024) void moe_build_pairs_kernel(const int32_t* ids,
-                                                               const float* w, int T,
-                                                               int topk, int n_experts,
-                                                               RouteTables rt) {
-    __shared__ int cnt[kMaxExperts];
-    __shared__ int scan[kMaxExperts];
-    __shared__ int sid[kMaxTokens * kMaxTopk];
-    const int tid = threadIdx.x;
-    const int n = T * topk;
-    if (tid < n_experts) cnt[tid] = 0;
-    for (int i = tid; i < n; i += blockDim.x) sid[i] = ids[i];
-    __syncthreads();
-    for (int i = tid; i < n; i += blockDim.x) {
-        const int e = sid[i];
-        if (e >= 0 && e < n_experts) atomicAdd(&cnt[e], 1);
+// Top-k of one token's logits on one wave: descending, ties to the lower
+// expert index, weights sigmoid(l) renormalised to sum 1. Lane k < topk
+// returns the k-th pick. Each lane holds PER logits (expert lane + 64*i);
+// each round takes the wave maximum (DPP), then the lowest index holding it;
+// a picked entry becomes NaN, which fmaxf and the comparisons ignore. NaN
+// logits rank as -inf.
+template <int PER>
+__device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk,
+                                                  int lane, int& my_e, float& my_w) {
+    const float kRemoved = __uint_as_float(0x7FC00000u);
+    float v[PER];
+    // Unconditional loads (index clamped into the row) so all of them are in
+    // flight together; entries past n_experts become "removed".
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        float l = lt[min(e, n_experts - 1)];
+        l = (l != l) ? -INFINITY : l;
+        v[i] = e < n_experts ? l : kRemoved;
     }
-    __syncthreads();
-    // Inclusive scan of (routed flag << 16 | count): both fields stay < 2^16.
-    const int c = tid < n_experts ? cnt[tid] : 0;
-    const int v = ((c > 0) << 16) | c;
-    scan[tid] = v;
-    __syncthreads();
-    for (int d = 1; d < kMaxExperts; d <<= 1) {
-        const int add = tid >= d ? scan[tid - d] : 0;
-        __syncthreads();
-        scan[tid] += add;
-        __syncthreads();
-    }
-    const int incl = scan[tid];
-    const int excl = incl - v;
-    if (c > 0) {
-        const int slot = excl >> 16;
-        const int poff = excl & 0xFFFF;
-        rt.uexp[slot] = tid;
-        rt.off[slot] = poff;
-        int k = 0;
-        for (int i = 0; i < n; ++i) {
-            if (sid[i] == tid) {
-                rt.pair_tok[poff + k] = i / topk;
-                rt.pair_w[poff + k] = w[i];
-                ++k;
-            }
+    my_e = 0;
+    float my_l = -INFINITY;
+    for (int k = 0; k < topk; ++k) {
+        float best = v[0];
+#pragma unroll
+        for (int i = 1; i < PER; ++i) best = fmaxf(best, v[i]);
+        const float wmax = wave_max_f32(best);
+        int idx = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = PER - 1; i >= 0; --i)
+            if (v[i] == wmax) idx = lane + 64 * i;
+        idx = wave_min_i32(idx);
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (lane + 64 * i == idx) v[i] = kRemoved;
+        if (lane == k) {
+            my_e = idx;
+            my_l = wmax;
         }
     }
-    if (tid == kMaxExperts - 1) {
+    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
+    my_w = s / wave_sum_f32(s);
+}
+
+__device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int lane,
+                                              int& e, float& w) {
+    if (n_experts <= 256) wave_topk_sigmoid<4>(lt, n_experts, topk, lane, e, w);
+    else if (n_experts <= 512) wave_topk_sigmoid<8>(lt, n_experts, topk, lane, e, w);
+    else wave_topk_sigmoid<16>(lt, n_experts, topk, lane, e, w);
+}
+
+constexpr int kRouteThreads = 256;
+constexpr int kExpPerThread = kMaxExperts / kRouteThreads;  // 4
+
+// One workgroup of 256 threads builds the routing tables of T tokens:
+//  1. ids/weights: top-k + sigmoid of the logits (one wave per token), or the
+//     caller's ids/weights;
+//  2. each (token, expert) pair is counted once per expert (an expert listed
+//     twice for one token forms one pair whose weight is the sum), and one
+//     scan over the experts gives each routed expert its slot (ascending
+//     expert id) and pair offset;
+//  3. each pair takes a position inside its expert's range with an LDS
+//     atomic. Positions inside one expert are unordered, which cannot change
+//     results: pairs of one expert belong to distinct tokens, and stage B
+//     accumulates every token separately.
+// All steps are data-parallel over the T*topk entries (no serial loops).
+// Ids outside [0, n_experts) are dropped.
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* logits,
+                                                                  const int32_t* ids_in,
+                                                                  const float* w_in, int T, int topk,
+                                                                  int n_experts, int32_t* ids_out,
+                                                                  float* w_out, RouteTables rt) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int scan[kRouteThreads / 64];
+    __shared__ int sid[kMaxTokens * kMaxTopk];
+    __shared__ float sw[kMaxTokens * kMaxTopk];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = T * topk;
+#pragma unroll
+    for (int q = 0; q < kExpPerThread; ++q) cnt[tid * kExpPerThread + q] = 0;
+    if (logits != nullptr) {
+        for (int t = wave; t < T; t += kRouteThreads / 64) {
+            int e;
+            float w;
+            wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, lane, e, w);
+            if (lane < topk) {
+                sid[t * topk + lane] = e;
+                sw[t * topk + lane] = w;
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += kRouteThreads) {
+            sid[i] = ids_in[i];
+            sw[i] = w_in[i];
+        }
+    }
+    __syncthreads();
+    // Per entry: is it the first listing of its expert in its token, and the
+    // summed weight of all listings (branch-free over the token's entries).
+    constexpr int kEntries = kMaxTokens * kMaxTopk / kRouteThreads;  // 4
+    bool take[kEntries];
+    float wsum[kEntries];
+#pragma unroll
+    for (int q = 0; q < kEntries; ++q) {
+        const int i = tid + q * kRouteThreads;
+        take[q] = false;
+        wsum[q] = 0.f;
+        if (i < n) {
+            const int e = sid[i];
+            const int t0 = (i / topk) * topk;
+            bool first = true;
+            float w = 0.f;
+            for (int k = 0; k < topk; ++k) {
+                const int ek = sid[t0 + k];
+                const float wk = sw[t0 + k];
+                first = first && !(t0 + k < i && ek == e);
+                w += (ek == e) ? wk : 0.f;
+            }
+            take[q] = first && e >= 0 && e < n_experts;
+            wsum[q] = w;
+            if (ids_out != nullptr) {
+                ids_out[i] = e;
+                w_out[i] = sw[i];
+            }
+            if (take[q]) atomicAdd(&cnt[e], 1);
+        }
+    }
+    __syncthreads();
+    // Thread tid owns experts 4*tid .. 4*tid+3. Scan of (routed flag << 16 |
+    // count) (both fields stay < 2^16): serial over the thread's experts, a
+    // shuffle scan inside each wave, then wave totals in wave order.
+    int c[kExpPerThread];
+    int local = 0;
+#pragma unroll
+    for (int q = 0; q < kExpPerThread; ++q) {
+        const int e = tid * kExpPerThread + q;
+        c[q] = e < n_experts ? cnt[e] : 0;
+        local += ((c[q] > 0) << 16) | c[q];
+    }
+    int incl = local;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int up = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += up;
+    }
+    if (lane == 63) scan[wave] = incl;
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) incl += scan[w];
+    int run = incl - local;
+#pragma unroll
+    for (int q = 0; q < kExpPerThread; ++q) {
+        const int e = tid * kExpPerThread + q;
+        if (c[q] > 0) {
+            rt.uexp[run >> 16] = e;
+            rt.off[run >> 16] = run & 0xFFFF;
+        }
+        if (e < n_experts) cnt[e] = run & 0xFFFF;  // next free pair position of expert e
+        run += ((c[q] > 0) << 16) | c[q];
+    }
+    if (tid == kRouteThreads - 1) {
         const int U = incl >> 16;
         const int P = incl & 0xFFFF;
         rt.header[0] = U;
         rt.header[1] = P;
         rt.off[U] = P;
     }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kEntries; ++q) {
+        const int i = tid + q * kRouteThreads;
+        if (take[q]) {
+            const int pos = atomicAdd(&cnt[sid[i]], 1);
+            rt.pair_tok[pos] = i / topk;
+            rt.pair_w[pos] = wsum[q];
+        }
+    }
 }
 
-// One wave per token: top-k of the logits (descending, ties to the lower
-// index) with weights sigmoid(l) renormalised to sum 1. Lane k keeps the k-th
-// pick; a picked entry becomes NaN, which never compares greater or equal.
+// Gating only: one wave per token writes ids [T, topk] and weights [T, topk].
 __global__ __launch_bounds__(64) void moe_route_sigmoid_topk_kernel(const float* logits,
                                                                      int n_experts, int topk,
                                                                      int32_t* ids, float* wout) {
     const int t = blockIdx.x;
     const int lane = threadIdx.x;
-    const float* lt = logits + (int64_t)t * n_experts;
-    constexpr int kPer = kMaxExperts / 64;
-    float v[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = lane + 64 * i;
-        const float l = e < n_experts ? lt[e] : __uint_as_float(0x7FC00000u);
-        v[i] = (e < n_experts && l != l) ? -INFINITY : l;  // NaN logit ranks last
-    }
-    int my_e = 0;
-    float my_l = -INFINITY;
-    for (int k = 0; k < topk; ++k) {
-        float best = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int e = lane + 64 * i;
-            if (v[i] > best || (v[i] == best && e < bi)) {
-                best = v[i];
-                bi = e;
-            }
-        }
-#pragma unroll
-        for (int m = 32; m > 0; m >>= 1) {
-            const float ob = __shfl_xor(best, m, 64);
-            const int oi = __shfl_xor(bi, m, 64);
-            if (ob > best || (ob == best && oi < bi)) {
-                best = ob;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (lane + 64 * i == bi) v[i] = __uint_as_float(0x7FC00000u);
-        if (lane == k) {
-            my_e = bi;
-            my_l = best;
-        }
-    }
-    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
-    const float tot = wave_sum(s);
+    int e;
+    float w;
+    wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, lane, e, w);
     if (lane < topk) {
-        ids[(int64_t)t * topk + lane] = my_e;
-        wout[(int64_t)t * topk + lane] = s / tot;
+        ids[(int64_t)t * topk + lane] = e;
+        wout[(int64_t)t * topk + lane] = w;
     }
 }
 
@@ -465,44 +796,131 @@ int env_int(const char* name, int def) {
     return v > 0 ? v : def;
 }
 
-// hidden rows per stage-A wave (multiple of kHpw); tunable for sweeps.
-int stage_a_rows_per_wave() {
-    static const int v = [] {
-        int r = env_int("DSV4_GROUPED_H_PER_WAVE", 8);
-        r = (r + kHpw - 1) / kHpw * kHpw;
-        return r;
+// Launch shapes. Stage A: hidden rows per chunk HC (2 or 4) and whether a
+// wave pipelines several chunks (PIPE, rows per wave from
+// DSV4_GROUPED_H_PER_WAVE) or owns exactly one. Stage B: output rows per
+// workgroup RB, waves per workgroup WB, pipelined expert slots or not.
+// Defaults come from sweeps on MI355X; the environment variables exist for
+// re-tuning (DSV4_GROUPED_HC, DSV4_GROUPED_PIPE, DSV4_GROUPED_H_PER_WAVE,
+// DSV4_GROUPED_B = RB*100 + WB*10 + PIPE, e.g. 880).
+struct Shapes {
+    int hc, pipe, h_per_wave;
+    int rb, wb, bpipe;
+    int t1, t1_waves, t1_xfirst;
+};
+
+const Shapes& shapes() {
+    static const Shapes s = [] {
+        Shapes v;
+        v.hc = env_int("DSV4_GROUPED_HC", 4) >= 4 ? 4 : 2;
+        v.pipe = env_int("DSV4_GROUPED_PIPE", 0) == 1 ? 1 : 0;
+        int r = env_int("DSV4_GROUPED_H_PER_WAVE", v.hc * 4);
+        v.h_per_wave = v.pipe ? (r + v.hc - 1) / v.hc * v.hc : v.hc;
+        const int b = env_int("DSV4_GROUPED_B", 880);
+        v.rb = (b / 100) >= 16 ? 16 : 8;
+        v.wb = ((b / 10) % 10) >= 8 ? 8 : 4;
+        v.bpipe = b % 10 == 1;
+        // One-token stage A: DSV4_GROUPED_T1 = waves*10 + xfirst (0 disables).
+        const int t1 = env_int("DSV4_GROUPED_T1", 41);
+        v.t1 = t1 >= 10;
+        v.t1_waves = t1 / 10 >= 16 ? 16 : (t1 / 10 >= 8 ? 8 : 4);
+        v.t1_xfirst = t1 % 10 == 1;
+        if (std::getenv("DSV4_GROUPED_T1") && std::atoi(std::getenv("DSV4_GROUPED_T1")) == 0) v.t1 = 0;
+        return v;
     }();
-    return v;
+    return s;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 uintptr_t align_up(uintptr_t v, uintptr_t a) { return (v + a - 1) / a * a; }
 
-template <bool INDEXED, bool ALIGNED>
-hipError_t launch_stage_a(const StageAArgs& a, int slots, hipStream_t stream) {
-    const int hpw = a.h_per_wave;
-    dim3 grid((unsigned)((a.hidden + kWavesA * hpw - 1) / (kWavesA * hpw)), (unsigned)slots);
+int blocks_per_lane(int K) { return (K / kBlkElems + 63) / 64; }
+
+// NB-byte scale loads are legal when every row's lane offset stays NB-aligned.
+int scale_vec_ok(int nb, int nblk, const void* s0, const void* s1) {
+    const uintptr_t m = (uintptr_t)nb - 1;
+    return nb > 1 && nblk % nb == 0 && (reinterpret_cast<uintptr_t>(s0) & m) == 0 &&
+           (reinterpret_cast<uintptr_t>(s1) & m) == 0;
+}
+
+// FAST kernels: 16-byte aligned operands, every lane owning NB whole blocks of
+// every row (K == 2048*NB) and NB-byte scale loads; other shapes take the
+// checked path (HC = 2, one chunk per wave).
+template <bool INDEXED, bool ALIGNED, bool MULTI>
+hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream) {
+    const Shapes& sh = shapes();
+    const int nb = blocks_per_lane(a.K);
+    a.scale_vec = scale_vec_ok(nb, a.K / kBlkElems, a.s1, a.s3);
+    const bool fast = ALIGNED && a.K == 2048 * nb && (nb == 1 || a.scale_vec);
+    const int hc = fast ? sh.hc : 2;
+    const bool pipe = fast && sh.pipe;
+    a.h_per_wave = pipe ? sh.h_per_wave : hc;
+    dim3 grid((unsigned)((a.hidden + kWavesA * a.h_per_wave - 1) / (kWavesA * a.h_per_wave)),
+              (unsigned)slots);
     dim3 block(64 * kWavesA);
-    const int nb = (a.K / kBlkElems + 63) / 64;
-    switch (nb) {
-        case 1: hipLaunchKernelGGL((moe_swiglu_kernel<1, INDEXED, ALIGNED>), grid, block, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((moe_swiglu_kernel<2, INDEXED, ALIGNED>), grid, block, 0, stream, a); break;
-        default: return hipErrorInvalidValue;
+#define DSV4_A(NBV, HCV, FASTV, PIPEV) \
+    hipLaunchKernelGGL((moe_swiglu_kernel<NBV, HCV, INDEXED, FASTV, PIPEV, MULTI>), grid, block, 0, stream, a)
+    if (fast && !MULTI && !pipe && sh.t1) {
+        const int W = sh.t1_waves;
+        dim3 g1((unsigned)((a.hidden + W * hc - 1) / (W * hc)), (unsigned)slots);
+#define DSV4_T1(NBV, HCV, WV, XF) \
+    hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, HCV, INDEXED, WV, XF>), g1, dim3(64 * WV), 0, stream, a)
+        if (nb == 1) DSV4_T1(1, 4, 4, true);
+        else if (W == 4 && sh.t1_xfirst) DSV4_T1(2, 4, 4, true);
+        else if (W == 4) DSV4_T1(2, 4, 4, false);
+        else if (W == 8 && sh.t1_xfirst) DSV4_T1(2, 4, 8, true);
+        else if (W == 8) DSV4_T1(2, 4, 8, false);
+        else if (sh.t1_xfirst) DSV4_T1(2, 4, 16, true);
+        else DSV4_T1(2, 4, 16, false);
+#undef DSV4_T1
+    } else if (!fast) {
+        if (nb == 1) DSV4_A(1, 2, false, false);
+        else if (nb == 2) DSV4_A(2, 2, false, false);
+        else return hipErrorInvalidValue;
+    } else if (nb == 1) {
+        DSV4_A(1, 4, true, false);
+    } else if (nb == 2) {
+        if (hc == 4 && pipe) DSV4_A(2, 4, true, true);
+        else if (hc == 4) DSV4_A(2, 4, true, false);
+        else if (pipe) DSV4_A(2, 2, true, true);
+        else DSV4_A(2, 2, true, false);
+    } else {
+        return hipErrorInvalidValue;
     }
+#undef DSV4_A
     return hipGetLastError();
 }
 
-template <int TMAX, bool INDEXED, bool ALIGNED>
-hipError_t launch_stage_b(const StageBArgs& a, hipStream_t stream) {
-    dim3 grid((unsigned)((a.out_dim + kRowsB - 1) / kRowsB));
-    dim3 block(64 * kWavesB);
-    const int nb = (a.hidden / kBlkElems + 63) / 64;
-    switch (nb) {
-        case 1: hipLaunchKernelGGL((moe_down_kernel<1, TMAX, INDEXED, ALIGNED>), grid, block, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((moe_down_kernel<2, TMAX, INDEXED, ALIGNED>), grid, block, 0, stream, a); break;
-        default: return hipErrorInvalidValue;
+template <int TMAX, bool INDEXED, bool ALIGNED, bool MULTI>
+hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
+    const Shapes& sh = shapes();
+    const int nb = blocks_per_lane(a.hidden);
+    a.scale_vec = scale_vec_ok(nb, a.hidden / kBlkElems, a.s2, a.s2);
+    const bool fast = ALIGNED && a.hidden == 2048 * nb && (nb == 1 || a.scale_vec);
+#define DSV4_B(NBV, RBV, WBV, FASTV, PIPEV)                                                        \
+    hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, FASTV, PIPEV, MULTI>),       \
+                       dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
+    if (!fast) {
+        if (nb == 1) DSV4_B(1, 8, 4, false, false);
+        else if (nb == 2) DSV4_B(2, 8, 4, false, false);
+        else return hipErrorInvalidValue;
+    } else if (nb == 2) {
+        DSV4_B(2, 8, 8, true, false);
+    } else if (nb == 1) {
+        const int key = sh.rb * 100 + sh.wb * 10 + sh.bpipe;
+        switch (key) {
+            case 840: DSV4_B(1, 8, 4, true, false); break;
+            case 841: DSV4_B(1, 8, 4, true, true); break;
+            case 881: DSV4_B(1, 8, 8, true, true); break;
+            case 1640: DSV4_B(1, 16, 4, true, false); break;
+            case 1680: DSV4_B(1, 16, 8, true, false); break;
+            default: DSV4_B(1, 8, 8, true, false); break;
+        }
+    } else {
+        return hipErrorInvalidValue;
     }
+#undef DSV4_B
     return hipGetLastError();
 }
 
@@ -524,6 +942,117 @@ MoeWorkspaceLayout moe_layout(int T, int topk, int n_experts, int hidden) {
     L.M = take(2 * P * (size_t)hidden);
     L.total = o + 256;  // slack to 256-align a caller pointer
     return L;
+}
+
+struct MoeCall {
+    RouteTables rt;
+    uint16_t* M;
+    ExpertSet es;
+};
+
+int moe_validate(int T, int topk, int n_experts, int K_in, int hidden, int out_dim) {
+    if (K_in % kBlkElems != 0 || K_in < kBlkElems) return -1;
+    if (hidden % kBlkElems != 0 || hidden < kBlkElems) return -2;
+    if (K_in > kMaxRed || hidden > kMaxRed) return -3;
+    if (T < 1 || T > kMaxTokens || topk < 1 || topk > kMaxTopk || n_experts < 1 ||
+        n_experts > kMaxExperts || out_dim < 1) {
+        std::fprintf(stderr, "mxfp4 moe: bad T=%d topk=%d n_experts=%d out_dim=%d\n", T, topk,
+                     n_experts, out_dim);
+        return -4;
+    }
+    return 0;
+}
+
+MoeCall moe_call(int T, int topk, int n_experts, int hidden, void* workspace) {
+    const MoeWorkspaceLayout L = moe_layout(T, topk, n_experts, hidden);
+    uint8_t* base = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(workspace), 256));
+    MoeCall c;
+    c.rt.header = reinterpret_cast<int32_t*>(base + L.header);
+    c.rt.uexp = reinterpret_cast<int32_t*>(base + L.uexp);
+    c.rt.off = reinterpret_cast<int32_t*>(base + L.off);
+    c.rt.pair_tok = reinterpret_cast<int32_t*>(base + L.pair_tok);
+    c.rt.pair_w = reinterpret_cast<float*>(base + L.pair_w);
+    c.M = reinterpret_cast<uint16_t*>(base + L.M);
+    c.es = ExpertSet{};
+    c.es.n_unique = c.rt.header;
+    c.es.uexp = c.rt.uexp;
+    c.es.off = c.rt.off;
+    c.es.pair_tok = c.rt.pair_tok;
+    c.es.pair_w = c.rt.pair_w;
+    const int P = T * topk;
+    c.es.n_slots = n_experts < P ? n_experts : P;
+    return c;
+}
+
+int launch_route(const float* logits, const int32_t* ids, const float* weights, int T, int topk,
+                 int n_experts, int32_t* ids_out, float* w_out, const MoeCall& c,
+                 hipStream_t stream) {
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, logits, ids,
+                       weights, T, topk, n_experts, ids_out, w_out, c.rt);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "mxfp4 moe: routing launch failed: %s\n", hipGetErrorString(e));
+        return -5;
+    }
+    return 0;
+}
+
+int launch_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed, const uint8_t* W3_packed,
+                  const uint8_t* W1_scale, const uint8_t* W3_scale, int K_in, int hidden, int T,
+                  const MoeCall& c, hipStream_t stream) {
+    StageAArgs A{};
+    A.x = reinterpret_cast<const uint16_t*>(x);
+    A.w1 = W1_packed;
+    A.w3 = W3_packed;
+    A.s1 = W1_scale;
+    A.s3 = W3_scale;
+    A.w_exp_stride = (int64_t)hidden * (K_in / 2);
+    A.s_exp_stride = (int64_t)hidden * (K_in / kBlkElems);
+    A.K = K_in;
+    A.hidden = hidden;
+    A.M = c.M;
+    A.es = c.es;
+    const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
+    hipError_t e;
+    if (T == 1)
+        e = al ? launch_stage_a<true, true, false>(A, c.es.n_slots, stream)
+               : launch_stage_a<true, false, false>(A, c.es.n_slots, stream);
+    else
+        e = al ? launch_stage_a<true, true, true>(A, c.es.n_slots, stream)
+               : launch_stage_a<true, false, true>(A, c.es.n_slots, stream);
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "mxfp4 moe: stage A launch failed: %s\n", hipGetErrorString(e));
+        return -6;
+    }
+    return 0;
+}
+
+int launch_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int hidden, int out_dim,
+                dsv4_bf16_t* out, const MoeCall& c, hipStream_t stream) {
+    StageBArgs B{};
+    B.M = c.M;
+    B.w2 = W2_packed;
+    B.s2 = W2_scale;
+    B.w_exp_stride = (int64_t)out_dim * (hidden / 2);
+    B.s_exp_stride = (int64_t)out_dim * (hidden / kBlkElems);
+    B.hidden = hidden;
+    B.out_dim = out_dim;
+    B.T = T;
+    B.out = reinterpret_cast<uint16_t*>(out);
+    B.es = c.es;
+    const bool al = aligned16(W2_packed);
+    hipError_t e;
+    if (T == 1)
+        e = al ? launch_stage_b<1, true, true, false>(B, stream)
+               : launch_stage_b<1, true, false, false>(B, stream);
+    else
+        e = al ? launch_stage_b<kMaxTokens, true, true, true>(B, stream)
+               : launch_stage_b<kMaxTokens, true, false, true>(B, stream);
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "mxfp4 moe: stage B launch failed: %s\n", hipGetErrorString(e));
+        return -7;
+    }
+    return 0;
 }
 
 }  // namespace
@@ -587,7 +1116,6 @@ extern "C" int mxfp4_grouped_gemv_topk(const dsv4_bf16_t* x, const uint8_t* W1_p
     A.s_exp_stride = (int64_t)hidden * (K_in / kBlkElems);
     A.K = K_in;
     A.hidden = hidden;
-    A.h_per_wave = stage_a_rows_per_wave();
     A.M = M;
     A.es = es;
 
@@ -605,13 +1133,14 @@ extern "C" int mxfp4_grouped_gemv_topk(const dsv4_bf16_t* x, const uint8_t* W1_p
 
     const bool al_a = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
     const bool al_b = aligned16(W2_packed);
-    hipError_t e = al_a ? launch_stage_a<false, true>(A, n_exp, stream)
-                        : launch_stage_a<false, false>(A, n_exp, stream);
+    hipError_t e = al_a ? launch_stage_a<false, true, false>(A, n_exp, stream)
+                        : launch_stage_a<false, false, false>(A, n_exp, stream);
     if (e != hipSuccess) {
         std::fprintf(stderr, "mxfp4 grouped: stage A launch failed: %s\n", hipGetErrorString(e));
         return -5;
     }
-    e = al_b ? launch_stage_b<1, false, true>(B, stream) : launch_stage_b<1, false, false>(B, stream);
+    e = al_b ? launch_stage_b<1, false, true, false>(B, stream)
+             : launch_stage_b<1, false, false, false>(B, stream);
     if (e != hipSuccess) {
         std::fprintf(stderr, "mxfp4 grouped: stage B launch failed: %s\n", hipGetErrorString(e));
         return -6;
@@ -641,64 +1170,13 @@ extern "C" size_t mxfp4_moe_workspace_bytes(int T, int topk, int n_experts, int 
     return moe_layout(T, topk, n_experts, hidden).total;
 }
 
-namespace {
-
-struct MoeCall {
-    RouteTables rt;
-    uint16_t* M;
-    ExpertSet es;
-};
-
-int moe_validate(int T, int topk, int n_experts, int K_in, int hidden, int out_dim) {
-    if (K_in % kBlkElems != 0 || K_in < kBlkElems) return -1;
-    if (hidden % kBlkElems != 0 || hidden < kBlkElems) return -2;
-    if (K_in > kMaxRed || hidden > kMaxRed) return -3;
-    if (T < 1 || T > kMaxTokens || topk < 1 || topk > kMaxTopk || n_experts < 1 ||
-        n_experts > kMaxExperts || out_dim < 1) {
-        std::fprintf(stderr, "mxfp4 moe: bad T=%d topk=%d n_experts=%d out_dim=%d\n", T, topk,
-                     n_experts, out_dim);
-        return -4;
-    }
-    return 0;
-}
-
-MoeCall moe_call(int T, int topk, int n_experts, int hidden, void* workspace) {
-    const MoeWorkspaceLayout L = moe_layout(T, topk, n_experts, hidden);
-    uint8_t* base = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(workspace), 256));
-    MoeCall c;
-    c.rt.header = reinterpret_cast<int32_t*>(base + L.header);
-    c.rt.uexp = reinterpret_cast<int32_t*>(base + L.uexp);
-    c.rt.off = reinterpret_cast<int32_t*>(base + L.off);
-    c.rt.pair_tok = reinterpret_cast<int32_t*>(base + L.pair_tok);
-    c.rt.pair_w = reinterpret_cast<float*>(base + L.pair_w);
-    c.M = reinterpret_cast<uint16_t*>(base + L.M);
-    c.es = ExpertSet{};
-    c.es.n_unique = c.rt.header;
-    c.es.uexp = c.rt.uexp;
-    c.es.off = c.rt.off;
-    c.es.pair_tok = c.rt.pair_tok;
-    c.es.pair_w = c.rt.pair_w;
-    const int P = T * topk;
-    c.es.n_slots = n_experts < P ? n_experts : P;
-    return c;
-}
-
-}  // namespace
-
 extern "C" int mxfp4_moe_build_routing(const int32_t* ids, const float* weights, int T, int topk,
                                        int n_experts, int hidden, void* workspace,
                                        hipStream_t stream) {
     const int v = moe_validate(T, topk, n_experts, kBlkElems, hidden, 1);
     if (v != 0) return v;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
-    hipLaunchKernelGGL(moe_build_pairs_kernel, dim3(1), dim3(kMaxExperts), 0, stream, ids, weights,
-                       T, topk, n_experts, c.rt);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        std::fprintf(stderr, "mxfp4 moe: routing launch failed: %s\n", hipGetErrorString(e));
-        return -5;
-    }
-    return 0;
+    return launch_route(nullptr, ids, weights, T, topk, n_experts, nullptr, nullptr, c, stream);
 }
 
 extern "C" int mxfp4_moe_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed,
@@ -708,27 +1186,7 @@ extern "C" int mxfp4_moe_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed,
     const int v = moe_validate(T, topk, n_experts, K_in, hidden, 1);
     if (v != 0) return v;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
-    StageAArgs A{};
-    A.x = reinterpret_cast<const uint16_t*>(x);
-    A.w1 = W1_packed;
-    A.w3 = W3_packed;
-    A.s1 = W1_scale;
-    A.s3 = W3_scale;
-    A.w_exp_stride = (int64_t)hidden * (K_in / 2);
-    A.s_exp_stride = (int64_t)hidden * (K_in / kBlkElems);
-    A.K = K_in;
-    A.hidden = hidden;
-    A.h_per_wave = stage_a_rows_per_wave();
-    A.M = c.M;
-    A.es = c.es;
-    const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
-    const hipError_t e = al ? launch_stage_a<true, true>(A, c.es.n_slots, stream)
-                            : launch_stage_a<true, false>(A, c.es.n_slots, stream);
-    if (e != hipSuccess) {
-        std::fprintf(stderr, "mxfp4 moe: stage A launch failed: %s\n", hipGetErrorString(e));
-        return -6;
-    }
-    return 0;
+    return launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
 }
 
 extern "C" int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int topk,
@@ -737,24 +1195,7 @@ extern "C" int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale,
     const int v = moe_validate(T, topk, n_experts, kBlkElems, hidden, out_dim);
     if (v != 0) return v;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
-    StageBArgs B{};
-    B.M = c.M;
-    B.w2 = W2_packed;
-    B.s2 = W2_scale;
-    B.w_exp_stride = (int64_t)out_dim * (hidden / 2);
-    B.s_exp_stride = (int64_t)out_dim * (hidden / kBlkElems);
-    B.hidden = hidden;
-    B.out_dim = out_dim;
-    B.T = T;
-    B.out = reinterpret_cast<uint16_t*>(out);
-    B.es = c.es;
-    const hipError_t e = aligned16(W2_packed) ? launch_stage_b<kMaxTokens, true, true>(B, stream)
-                                              : launch_stage_b<kMaxTokens, true, false>(B, stream);
-    if (e != hipSuccess) {
-        std::fprintf(stderr, "mxfp4 moe: stage B launch failed: %s\n", hipGetErrorString(e));
-        return -7;
-    }
-    return 0;
+    return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
 }
 
 extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_packed,
@@ -766,11 +1207,28 @@ extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_pa
                                       void* workspace, hipStream_t stream) {
     int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
     if (v != 0) return v;
-    v = mxfp4_moe_build_routing(ids, weights, T, topk, n_experts, hidden, workspace, stream);
+    const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
+    v = launch_route(nullptr, ids, weights, T, topk, n_experts, nullptr, nullptr, c, stream);
     if (v != 0) return v;
-    v = mxfp4_moe_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, T, topk, n_experts, K_in,
-                         hidden, workspace, stream);
+    v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
     if (v != 0) return v;
-    return mxfp4_moe_down(W2_packed, W2_scale, T, topk, n_experts, hidden, out_dim, out, workspace,
-                          stream);
+    return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+}
+
+extern "C" int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
+                               const uint8_t* W1_packed, const uint8_t* W3_packed,
+                               const uint8_t* W2_packed, const uint8_t* W1_scale,
+                               const uint8_t* W3_scale, const uint8_t* W2_scale, int T, int topk,
+                               int n_experts, int K_in, int hidden, int out_dim, dsv4_bf16_t* out,
+                               int32_t* ids_out, float* weights_out, void* workspace,
+                               hipStream_t stream) {
+    int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
+    if (v != 0) return v;
+    if (topk > n_experts) return -4;
+    const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
+    v = launch_route(logits, nullptr, nullptr, T, topk, n_experts, ids_out, weights_out, c, stream);
+    if (v != 0) return v;
+    v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
+    if (v != 0) return v;
+    return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
 }

@@ -85,8 +85,10 @@ def expert_host_weights(seed_base: int, e: int, K: int, hidden: int, out_dim: in
 class RoutedMoELayer:
     """Device-resident routed MoE layer: forward(x, logits) -> bf16 [T, out_dim]."""
 
-    def __init__(self, weights: MoEWeights, topk: int = 8, max_tokens: int = 16):
+    def __init__(self, weights: MoEWeights, topk: int = 8, max_tokens: int = 16,
+                 check: bool = True):
         self.w = weights
+        self.check = check
         self.topk = topk
         self.max_tokens = max_tokens
         dev = weights.W1["packed"].device
@@ -110,7 +112,10 @@ class RoutedMoELayer:
         if T > self.max_tokens:
             raise ValueError(f"T={T} > max_tokens={self.max_tokens}")
         if logits is not None:
-            ids, weights = self.route(logits)
+            return gb.mxfp4_moe_layer(x, logits, self.w.W1, self.w.W3, self.w.W2, self.topk,
+                                      out=self.out[:T], ids_out=self.ids[:T],
+                                      weights_out=self.weights[:T], workspace=self.workspace,
+                                      check=self.check)
         if ids is None or weights is None:
             raise ValueError("pass logits, or ids and weights")
         return gb.mxfp4_moe_grouped_gemv(x, self.w.W1, self.w.W3, self.w.W2, ids, weights,

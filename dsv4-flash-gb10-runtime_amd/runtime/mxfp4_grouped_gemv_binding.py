@@ -61,6 +61,8 @@ def _load_lib() -> ctypes.CDLL:
     lib.mxfp4_moe_swiglu.argtypes = [_c_void_p] * 5 + [_c_int] * 5 + [_c_void_p] * 2
     lib.mxfp4_moe_down.restype = _c_int
     lib.mxfp4_moe_down.argtypes = [_c_void_p] * 2 + [_c_int] * 5 + [_c_void_p] * 3
+    lib.mxfp4_moe_layer.restype = _c_int
+    lib.mxfp4_moe_layer.argtypes = [_c_void_p] * 8 + [_c_int] * 6 + [_c_void_p] * 5
     _LIB = lib
     return lib
 
@@ -224,6 +226,65 @@ def mxfp4_moe_grouped_gemv(
     return out
 
 
+def mxfp4_moe_layer(
+    x: torch.Tensor,
+    logits: torch.Tensor,
+    W1: Dict[str, torch.Tensor],
+    W3: Dict[str, torch.Tensor],
+    W2: Dict[str, torch.Tensor],
+    topk: int,
+    out: Optional[torch.Tensor] = None,
+    ids_out: Optional[torch.Tensor] = None,
+    weights_out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+    check: bool = True,
+) -> torch.Tensor:
+    """Routed-MoE layer at decode in one library call: device gating of logits
+    [T, E] + expert-indexed grouped GEMV; returns bf16 [T, out_dim].
+    `check=False` skips the Python-side validation (the library still
+    validates shapes) for callers that reuse checked buffers in a loop."""
+    lib = _load_lib()
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    T, K_in = x.shape
+    n_experts, hidden = W1["packed"].shape[0], W1["packed"].shape[1]
+    out_dim = W2["packed"].shape[1]
+    if check:
+        _check(x, "x", torch.bfloat16)
+        _check(logits, "logits", torch.float32)
+        _check_mats(W1, W3, W2)
+        _shapes(W1, W3, W2, K_in)
+        if tuple(logits.shape) != (T, n_experts):
+            raise ValueError(f"logits shape {tuple(logits.shape)} != ({T}, {n_experts})")
+    if out is None:
+        out = torch.empty(T, out_dim, dtype=torch.bfloat16, device=x.device)
+    if workspace is None:
+        workspace = torch.empty(lib.mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden),
+                                dtype=torch.uint8, device=x.device)
+    if check:
+        _check(out, "out", torch.bfloat16)
+        if out.numel() != T * out_dim:
+            raise ValueError(f"out numel {out.numel()} != {T * out_dim}")
+        need = lib.mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden)
+        if workspace.numel() * workspace.element_size() < need:
+            raise ValueError(f"workspace smaller than {need} bytes")
+        for name, t, dt in (("ids_out", ids_out, torch.int32), ("weights_out", weights_out, torch.float32)):
+            if t is not None:
+                _check(t, name, dt)
+                if t.numel() != T * topk:
+                    raise ValueError(f"{name} numel {t.numel()} != {T * topk}")
+    rc = lib.mxfp4_moe_layer(
+        _lib.vp(x), _lib.vp(logits), _lib.vp(W1["packed"]), _lib.vp(W3["packed"]),
+        _lib.vp(W2["packed"]), _lib.vp(W1["scale"]), _lib.vp(W3["scale"]), _lib.vp(W2["scale"]),
+        T, topk, n_experts, K_in, hidden, out_dim, _lib.vp(out),
+        None if ids_out is None else _lib.vp(ids_out),
+        None if weights_out is None else _lib.vp(weights_out),
+        _lib.vp(workspace), ctypes.c_void_p(_lib.stream_ptr(x.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_layer returned {rc}")
+    return out
+
+
 class MoEStages:
     """The three launches of mxfp4_moe_grouped_gemv, callable one by one on a
     fixed workspace (preallocated here): build_routing(ids, weights) ->
@@ -264,5 +325,5 @@ class MoEStages:
         return out
 
 
-__all__ = ["mxfp4_grouped_gemv", "MoEStages", "MXFP4_BLOCK_ELEMS", "route_sigmoid_topk",
+__all__ = ["mxfp4_grouped_gemv", "MoEStages", "mxfp4_moe_layer", "MXFP4_BLOCK_ELEMS", "route_sigmoid_topk",
            "mxfp4_moe_grouped_gemv", "moe_workspace_bytes", "workspace_bytes"]

@@ -122,6 +122,19 @@ int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int
                    int n_experts, int hidden, int out_dim, dsv4_bf16_t* out, void* workspace,
                    hipStream_t stream);
 
+/* EXTENSION: one routed-MoE layer at decode in one call (three launches on
+ * `stream`): device gating of logits [T, n_experts] (top-`topk`, sigmoid
+ * weights renormalised to 1, as mxfp4_moe_route_sigmoid_topk), then stages A
+ * and B of mxfp4_moe_grouped_gemv. ids_out / weights_out ([T, topk], may be
+ * NULL) receive the routing. Workspace as mxfp4_moe_grouped_gemv. Return codes
+ * as mxfp4_moe_grouped_gemv (-4 also for topk > n_experts). */
+int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
+                    const uint8_t* W1_packed, const uint8_t* W3_packed, const uint8_t* W2_packed,
+                    const uint8_t* W1_scale, const uint8_t* W3_scale, const uint8_t* W2_scale,
+                    int T, int topk, int n_experts, int K_in, int hidden, int out_dim,
+                    dsv4_bf16_t* out, int32_t* ids_out, float* weights_out, void* workspace,
+                    hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* libmxfp4_gemv.so                                                          */
 /* ------------------------------------------------------------------------ */

@@ -19,7 +19,7 @@ LIBS = {
     "mxfp4-routed/libmxfp4_grouped_gemv.so": [
         "mxfp4_grouped_gemv_topk", "mxfp4_grouped_workspace_bytes",
         "mxfp4_moe_route_sigmoid_topk", "mxfp4_moe_workspace_bytes", "mxfp4_moe_grouped_gemv",
-        "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down"],
+        "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_dequant_bf16"],
     "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],

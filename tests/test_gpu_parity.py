@@ -314,3 +314,29 @@ def test_rmsnorm_scalar_path_and_noop(device):
     gw = dev_bf16(np.full(64, 0x3F80, np.uint16), device)
     yc = mx.bf16_to_f32(host_bits(rb.rmsnorm_fuse_fwd(c, gw)))
     assert np.allclose(yc, 0.75 / np.sqrt(0.75 ** 2 + 1e-6), rtol=4e-3)
+
+
+# ------------------------------------------------------------- HIP graphs ---
+
+def test_moe_layer_graph_replays_match_eager(device):
+    """A captured decode layer (gating + stages A/B, no memsets) replays
+    bit-identically to the eager call, with eager work between replays."""
+    from runtime import moe
+
+    E, K, H, O, T = 32, 1024, 512, 1024, 2
+    announce(f"mxfp4_moe_layer graph capture T={T} E={E}")
+    weights = moe.make_moe_weights(9700, E, K, H, O, device)
+    layer = moe.RoutedMoELayer(weights, topk=8, max_tokens=4)
+    x = dev_bf16(synth.normal_bf16(9701, (T, K)), device)
+    logits = dev_f32(synth.gating_logits(9702, T, E), device)
+    eager = host_bits(layer.forward(x, logits=logits)).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer.forward(x, logits=logits)
+    other = dev_f32(synth.gating_logits(9703, T, E), device)
+    for rep in range(4):
+        layer.out.zero_()
+        g.replay()
+        assert np.array_equal(host_bits(layer.out[:T]), eager), f"replay {rep}"
+        layer.forward(x, logits=other)  # eager work between replays
+        torch.cuda.synchronize()
