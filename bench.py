@@ -42,6 +42,7 @@ E, K, H, O, TOPK = 256, 4096, 2048, 4096, 8
 EXPERT_BYTES = 3 * (H * K // 2 + H * K // 32)          # 13,369,344 B (W1 + W3 + W2, packed + scales)
 STAGE_A_EXPERT_BYTES = 2 * (H * K // 2 + H * K // 32)  # 8,912,896 B (W1 + W3)
 STAGE_B_EXPERT_BYTES = O * H // 2 + O * H // 32         # 4,456,448 B (W2)
+STAGE_A_KERNEL = "moe_swiglu_t1_kernel"                  # stage A's kernel at T=1
 
 
 def log(msg: str) -> None:
@@ -50,6 +51,25 @@ def log(msg: str) -> None:
 
 def topk_ids(logits: np.ndarray) -> np.ndarray:
     return np.argsort(-logits.astype(np.float64), axis=1, kind="stable")[:, :TOPK]
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` as measured by rocprofv3 counter passes
+    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy of
+    known size). The summaries live in profiles/*.md as lines
+    `TRAFFIC <kernel> <bytes>`; returns (bytes, file) or (None, None)."""
+    d = os.path.join(REPO, "profiles")
+    if not os.path.isdir(d):
+        return None, None
+    for name in sorted(os.listdir(d)):
+        if not name.endswith(".md"):
+            continue
+        with open(os.path.join(d, name)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "TRAFFIC" and parts[1] == kernel:
+                    return int(parts[2]), "profiles/" + name
+    return None, None
 
 
 def cpu_model() -> str:
@@ -171,6 +191,16 @@ def main() -> int:
     b_bytes = float(np.mean(uniq[:R] * STAGE_B_EXPERT_BYTES + T * TOPK * H * 2 + T * O * 2))
     a_gbs = a_bytes / (a_us * 1e-6) / 1e9
     b_gbs = b_bytes / (b_us * 1e-6) / 1e9
+    del ga, gbr, stages
+
+    # --- measured device-copy ceiling: torch's copy kernel over 1 GiB (read + write) ---
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    dst.copy_(src)
+    copy_ms = timed(lambda: [dst.copy_(src) for _ in range(5)]) / 5
+    copy_gbs = 2 * src.numel() / (copy_ms * 1e-3) / 1e9
+    del src, dst
 
     # --- CPU baseline: the oracle (dequant + fp32 matmul) on step 0's experts ---
     cpu = None
@@ -218,6 +248,7 @@ def main() -> int:
         }
         del ids0
 
+    traffic, traffic_src = profiled_traffic(STAGE_A_KERNEL)
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -241,16 +272,18 @@ def main() -> int:
         "moe_layer_us": round(ms_per_step * 1e3, 3),
         "moe_layer_us_eager": round(ms_per_step_eager * 1e3, 3),
         "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        "copy_ceiling_gbs": round(copy_gbs, 1),
         "stage_us": {"swiglu_A": round(a_us, 3), "down_B": round(b_us, 3)},
         "stage_gbs": {"swiglu_A": round(a_gbs, 1), "down_B": round(b_gbs, 1)},
         "roofline": {
-            "kernel": "moe_swiglu_kernel (stage A: W1+W3 MXFP4 GEMV + SiLU)",
+            "kernel": f"{STAGE_A_KERNEL} (stage A: W1+W3 MXFP4 GEMV + SiLU)",
             "bound": "hbm",
             "achieved": round(a_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(a_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": int(round(a_bytes)),
             "avg_launch_us": round(a_us, 3),
         },

@@ -208,17 +208,20 @@ def grouped_gemv_topk(x, W1p, W3p, W2p, W1s, W3s, W2s, r) -> np.ndarray:
     return bf16_round(acc)
 
 
-def moe_layer(x, expert_fn, ids, weights, out_dim: int) -> np.ndarray:
+def moe_layer(x, expert_fn, ids, weights, out_dim: int, n_experts=None) -> np.ndarray:
     """out[t] = bf16( sum_k w[t,k] * W2_e . bf16(silu(W1_e x_t) * (W3_e x_t)) ),
     e = ids[t,k] (runtime/dsv4_engine_mxfp4.py:372-423 with the grouped kernel
     per token). expert_fn(e) -> ((W1p, W1s), (W3p, W3s), (W2p, W2s)).
-    Each unique expert is dequantised once. Ids outside [0, E) are skipped."""
+    Each unique expert is dequantised once. With n_experts given, ids outside
+    [0, n_experts) contribute nothing (the device entry skips them)."""
     x = np.atleast_2d(np.asarray(x, dtype=np.uint16))
     ids = np.asarray(ids)
     weights = np.asarray(weights, dtype=np.float32)
     T = x.shape[0]
     acc = np.zeros((T, out_dim), dtype=np.float32)
     for e in np.unique(ids):
+        if n_experts is not None and not 0 <= e < n_experts:
+            continue
         tok, kk = np.nonzero(ids == e)
         (W1p, W1s), (W3p, W3s), (W2p, W2s) = expert_fn(int(e))
         M = expert_swiglu_m(x[tok], W1p, W1s, W3p, W3s)

@@ -224,6 +224,34 @@ def test_moe_indexed_small_dims(device, T):
     assert_close(host_bits(out), mx.moe_layer(x, fn, ids, w, O), f"moe T={T}")
 
 
+def test_moe_duplicate_and_out_of_range_ids(device):
+    """A token listing one expert twice gets both contributions; ids outside
+    [0, n_experts) (negative or too large) contribute nothing."""
+    E, K, H, O, T, topk = 16, 512, 128, 256, 3, 4
+    announce(f"mxfp4_moe_grouped_gemv duplicate/invalid ids T={T} E={E}")
+    W1p, W1s = synth.mxfp4_weight(8300, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8304, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8308, O, H, E)
+    x = synth.normal_bf16(8310, (T, K))
+    ids = np.array([[3, 3, 5, 15], [-1, 2, 16, 2], [7, 1000, 0, 7]], np.int32)
+    w = np.array([[0.4, 0.3, 0.2, 0.1], [0.5, 0.25, 0.15, 0.1], [0.6, 0.2, 0.1, 0.1]], np.float32)
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    out = gb.mxfp4_moe_grouped_gemv(dev_bf16(x, device), W1, W3, W2,
+                                    torch.from_numpy(ids).to(device), dev_f32(w, device))
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    ref = mx.moe_layer(x, fn, ids, w, O, n_experts=E)
+    assert_close(host_bits(out), ref, "moe duplicate/invalid ids")
+    # the duplicate listing equals one listing with the summed weight
+    ids1 = np.array([[3, 5, 15, 15]], np.int32)
+    w1 = np.array([[0.7, 0.2, 0.1, 0.0]], np.float32)
+    out1 = gb.mxfp4_moe_grouped_gemv(dev_bf16(x[:1], device), W1, W3, W2,
+                                     torch.from_numpy(ids1).to(device), dev_f32(w1, device))
+    assert_close(host_bits(out1), host_bits(out)[:1], "duplicate merge", cos_tol=0.99999)
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_indexed_config_dims(device, T):
     """Config-3 shapes (256 experts, K=4096, H=2048, O=4096) with device-filled weights."""
@@ -298,6 +326,20 @@ def test_rmsnorm_residual_config(device, T):
     announce(f"rmsnorm_fuse_fwd T={T} H={H}")
     y2 = rb.rmsnorm_fuse_fwd(dev_bf16(h, device), dev_bf16(g, device))
     assert_close(host_bits(y2), mx.rmsnorm(h, g), f"rmsnorm fwd T={T}")
+
+
+def test_rmsnorm_max_hidden(device):
+    H, T = 8192, 2  # the largest hidden both entries accept
+    announce(f"rmsnorm_fuse_residual_add T={T} H={H}")
+    h = synth.normal_bf16(1401, (T, H))
+    r = synth.normal_bf16(1402, (T, H), 0.0, 0.5)
+    g = synth.normal_bf16(1403, (H,), 1.0, 0.1)
+    y, nr = rb.rmsnorm_fuse_residual_add(dev_bf16(h, device), dev_bf16(r, device), dev_bf16(g, device))
+    ry, rnr = mx.rmsnorm_residual(h, r, g)
+    assert np.array_equal(host_bits(nr), rnr)
+    assert_close(host_bits(y), ry, "rmsnorm H=8192")
+    assert_close(host_bits(rb.rmsnorm_fuse_fwd(dev_bf16(h, device), dev_bf16(g, device))),
+                 mx.rmsnorm(h, g), "rmsnorm fwd H=8192")
 
 
 def test_rmsnorm_scalar_path_and_noop(device):
