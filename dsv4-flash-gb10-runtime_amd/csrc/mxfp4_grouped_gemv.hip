@@ -66,7 +66,31 @@ struct ExpertSet {
     const float* pair_w;
     const float* rweights;
     int n_slots;
+    int n_pairs;                // rows of M / entries of pair_tok, pair_w (indexed)
+    int n_experts;              // experts of the per-layer tensors (indexed)
 };
+
+// Slot u of a one-pair-per-slot launch (T == 1), with every table read
+// unconditional and independent, so the weight loads that depend on the
+// expert id are issued after a single round trip. Tables past the routed
+// slots hold valid ids (the routing kernel fills them), and the ids and pair
+// index are clamped into range anyway; `valid` says whether the slot is routed.
+template <bool INDEXED>
+__device__ __forceinline__ void slot_info_t1(const ExpertSet& s, int u, int& expert, int& pbeg,
+                                             float& w, bool& valid) {
+    if constexpr (INDEXED) {
+        const int U = *s.n_unique;
+        expert = min(max(s.uexp[u], 0), s.n_experts - 1);
+        pbeg = min(max(s.off[u], 0), s.n_pairs - 1);
+        w = s.pair_w[pbeg];
+        valid = u < U;
+    } else {
+        expert = u;
+        pbeg = u;
+        w = s.rweights[u];
+        valid = u < s.n_slots;
+    }
+}
 
 template <bool INDEXED>
 __device__ __forceinline__ bool slot_info(const ExpertSet& s, int u, int& expert, int& pbeg,
@@ -335,62 +359,100 @@ __global__ __launch_bounds__(64 * kWavesA, PIPE ? 1 : 4) void moe_swiglu_kernel(
 }
 
 // One token (T = 1, or the drop-in entry) on the FAST path: a workgroup of
-// kT1Waves waves covers kT1Waves*HC hidden rows of one routed expert. The
-// workgroup stages the token's activation in LDS once (one 16-byte load per
-// thread; before or after the weight loads are issued, XFIRST) and every lane
-// copies its slice into registers, so the activation costs one L2 read per
-// workgroup instead of one per wave. Rows past `hidden` are clamped (loaded,
-// not stored) so every wave reaches the barrier.
-template <int NB, int HC, bool INDEXED, int kT1Waves, bool XFIRST>
+// kT1Waves waves covers R = kT1Waves*HC consecutive hidden rows of one expert
+// slot. Lane l owns MX blocks l, l+64, ... of each row, so every 16-byte
+// weight load instruction of a wave reads one contiguous KiB of a row. Each
+// thread first issues its share of the token's activation and of the
+// workgroup's scale tile (R rows x K/32 bytes of W1 and of W3, 16 bytes per
+// thread), then its wave's weight loads (unconditional, rows clamped), and
+// only then writes activation and scales to LDS: the wait covers the oldest
+// loads only, so the weight stream starts at once. Rows past `hidden` and
+// unrouted slots are loaded but not stored.
+template <int NB, int HC, bool INDEXED, int kT1Waves, int D>
 __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const StageAArgs a) {
+    constexpr int kThreads = 64 * kT1Waves;
+    constexpr int kRows = kT1Waves * HC;
+    constexpr int kXPer = (kMaxRed / 8 + kThreads - 1) / kThreads;  // 16-byte x pieces per thread
+    constexpr int kSTile = 2 * kRows * (kMaxRed / kBlkElems);          // scale tile bytes (max K)
+    constexpr int kSPer = (kSTile / 16 + kThreads - 1) / kThreads;     // 16-byte scale pieces per thread
     __shared__ u32x4 xl[kMaxRed * 2 / 16];
+    __shared__ u32x4 sl[kSTile / 16];
+    const uint8_t* slb = reinterpret_cast<const uint8_t*>(sl);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    int expert, pbeg, pend;
-    if (!slot_info<INDEXED>(a.es, blockIdx.y, expert, pbeg, pend)) return;  // whole workgroup
-    const int h0 = (blockIdx.x * kT1Waves + wave) * HC;
+    int expert, pbeg;
+    float wt;
+    bool valid;
+    slot_info_t1<INDEXED>(a.es, blockIdx.y, expert, pbeg, wt, valid);
+    (void)wt;
+    const int hw = blockIdx.x * kRows;        // first row of the workgroup (hidden % kRows == 0)
+    const int h0 = hw + wave * HC;
     const int K = a.K;
     const int nblk = K / kBlkElems;
     const int64_t wrow = K / 2;
-    const int b0 = NB * lane;
     const uint8_t* W1 = a.w1 + (int64_t)expert * a.w_exp_stride;
     const uint8_t* W3 = a.w3 + (int64_t)expert * a.w_exp_stride;
-    const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride;
-    const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride;
+    const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
+    const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
 
-    int tok;
-    float wt;
-    pair_info<INDEXED>(a.es, pbeg, tok, wt);
-    const u32x4* xg = reinterpret_cast<const u32x4*>(a.x + (int64_t)tok * K);
-    if constexpr (XFIRST) {
-        for (int i = threadIdx.x; i < K / 8; i += 64 * kT1Waves) xl[i] = xg[i];
-        __syncthreads();
-    }
-    GateUpChunk<NB, HC> c;
+    const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);  // token 0
+    const int nx = K / 8;
+    const int ns = kRows * nblk / 16;                        // 16-byte scale pieces per matrix
+    u32x4 xv[kXPer];
+    u32x4 sv[kSPer];
 #pragma unroll
-    for (int r = 0; r < HC; ++r) {
-        const int h = min(h0 + r, a.hidden - 1);
-        const int64_t so = (int64_t)h * nblk + b0;
+    for (int i = 0; i < kXPer; ++i) xv[i] = xg[min((int)threadIdx.x + kThreads * i, nx - 1)];
+#pragma unroll
+    for (int i = 0; i < kSPer; ++i) {
+        const int t = min((int)threadIdx.x + kThreads * i, 2 * ns - 1);
+        const uint8_t* src = t < ns ? S1 + 16 * t : S3 + 16 * (t - ns);
+        sv[i] = *reinterpret_cast<const u32x4*>(src);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation and scale loads oldest
+
+    GateUpChunk<NB, HC> c;
+    auto load_row = [&](int r) {
+        const int h = h0 + r;
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int64_t wo = (int64_t)h * wrow + (int64_t)(b0 + j) * 16;
+            const int64_t wo = (int64_t)h * wrow + (int64_t)(lane + 64 * j) * 16;
             c.w1[r][j] = ld16_stream(W1 + wo);
             c.w3[r][j] = ld16_stream(W3 + wo);
         }
-        c.s1[r] = load_scales<NB>(S1 + so, true, NB);
-        c.s3[r] = load_scales<NB>(S3 + so, true, NB);
+    };
+    // The first D rows are in flight before any compute; row r+D is issued
+    // right after row r is reduced.
+#pragma unroll
+    for (int r = 0; r < D; ++r) load_row(r);
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+        const int idx = threadIdx.x + kThreads * i;
+        if (idx < nx) xl[idx] = xv[i];
     }
-
-    if constexpr (!XFIRST) {
-        for (int i = threadIdx.x; i < K / 8; i += 64 * kT1Waves) xl[i] = xg[i];
-        __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSPer; ++i) {
+        const int idx = threadIdx.x + kThreads * i;
+        if (idx < 2 * ns) sl[idx] = sv[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < HC; ++r) {
+        const int row = wave * HC + r;
+        uint32_t p1 = 0, p3 = 0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            p1 |= (uint32_t)slb[row * nblk + lane + 64 * j] << (8 * j);
+            p3 |= (uint32_t)slb[kRows * nblk + row * nblk + lane + 64 * j] << (8 * j);
+        }
+        c.s1[r] = p1;
+        c.s3[r] = p3;
     }
     uint32_t xs[NB][16];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const u32x4 v = xl[(b0 + j) * 4 + q];
+            const u32x4 v = xl[(lane + 64 * j) * 4 + q];
             xs[j][4 * q + 0] = v[0];
             xs[j][4 * q + 1] = v[1];
             xs[j][4 * q + 2] = v[2];
@@ -413,11 +475,16 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         }
         g[r] = gg;
         u[r] = uu;
+        if (r + D < HC) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_row(r + D);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     wave_reduce_n<HC>(g, lane);
     wave_reduce_n<HC>(u, lane);
     const int r = reduced_index<HC>(lane);
-    if (reduced_owner<HC>(lane) && h0 + r < a.hidden)
+    if (valid && reduced_owner<HC>(lane) && h0 + r < a.hidden)
         a.M[(int64_t)pbeg * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
 }
 
@@ -433,9 +500,20 @@ struct StageBArgs {
     int out_dim;
     int T;
     int scale_vec;
+    int stage_scales;           // one-token path: scale rows staged per wave (out_dim % 8 == 0, 16-byte aligned)
     uint16_t* out;              // [T, out_dim] bf16
     ExpertSet es;
 };
+
+// A lane's share of a wave's staged scale rows: 8, 16 (or 4) bytes.
+template <int BYTES>
+struct ScalePiece;
+template <>
+struct ScalePiece<4> { typedef uint32_t type; };
+template <>
+struct ScalePiece<8> { typedef uint64_t type; };
+template <>
+struct ScalePiece<16> { typedef u32x4 type; };
 
 template <int NBB, int RB>
 struct DownRows {
@@ -449,12 +527,13 @@ struct DownRows {
 // the prefetch is unconditional: past the last slot it re-reads the current
 // rows); partial sums per (wave, token, row) meet in LDS and are added in wave
 // order.
-template <int NBB, int RB, int WB, int TMAX, bool INDEXED, bool FAST, bool PIPE, bool MULTI>
+template <int NBB, int RB, int WB, int TMAX, bool INDEXED, bool FAST, bool PIPE, bool MULTI, int BD = RB>
 __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_down_kernel(const StageBArgs a) {
     constexpr bool ALIGNED = FAST;
     constexpr int kRowsB = RB;
     constexpr int kWavesB = WB;
     __shared__ float acc[kWavesB][TMAX][kRowsB];
+    __shared__ __align__(16) uint8_t sstage[(!PIPE && !MULTI && FAST) ? kWavesB : 1][kRowsB * 64 * NBB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int o0 = blockIdx.x * kRowsB;
@@ -544,7 +623,78 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
 
     DownRows<NBB, RB> da, db;
     int u = wave;
-    if (!PIPE) {
+    if (!PIPE && !MULTI && FAST) {
+        // One pair per slot (T == 1): the slot's M slice is loaded before its
+        // W2 rows, so the row dots start as soon as the first row arrives; the
+        // table reads are unconditional (slot_info_t1) and unrouted slots are
+        // computed but not accumulated.
+#pragma unroll 1
+        for (; u < a.es.n_slots; u += kWavesB) {
+            int expert, pbeg;
+            float wt;
+            bool valid;
+            slot_info_t1<INDEXED>(a.es, u, expert, pbeg, wt, valid);
+            uint32_t ms[NBB][16];
+#pragma unroll
+            for (int j = 0; j < NBB; ++j)
+                load_act_block<true>(a.M + (int64_t)pbeg * a.hidden + (b0 + j) * kBlkElems, ms[j]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the M loads oldest
+            const uint8_t* W2 = a.w2 + (int64_t)expert * a.w_exp_stride;
+            const uint8_t* S2 = a.s2 + (int64_t)expert * a.s_exp_stride;
+            // The wave's kRowsB scale rows (kRowsB * nblk contiguous bytes) in
+            // one load of kRowsB*NBB bytes per lane, instead of one small load
+            // per row; redistributed through the wave's LDS slot below.
+            using SPiece = typename ScalePiece<kRowsB * NBB>::type;
+            SPiece spiece{};
+            if (a.stage_scales)
+                spiece = *reinterpret_cast<const SPiece*>(S2 + (int64_t)o0 * nblk + lane * (kRowsB * NBB));
+            __builtin_amdgcn_sched_barrier(0);
+            auto load_row = [&](int r) {
+                const int o = min(o0 + r, a.out_dim - 1);
+#pragma unroll
+                for (int j = 0; j < NBB; ++j)
+                    da.w[r][j] = ld16_stream(W2 + (int64_t)o * wrow + (int64_t)(b0 + j) * 16);
+                if (!a.stage_scales) da.s[r] = load_scales<NBB>(S2 + (int64_t)o * nblk + b0, true, NBB);
+            };
+            // BD rows in flight before the first dot; row r+BD is issued after
+            // row r's dot.
+#pragma unroll
+            for (int r = 0; r < BD; ++r) load_row(r);
+            if (a.stage_scales) {
+                SPiece* slot = reinterpret_cast<SPiece*>(&sstage[wave][0]);
+                slot[lane] = spiece;
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int r = 0; r < kRowsB; ++r) {
+                    uint32_t v = 0;
+#pragma unroll
+                    for (int j = 0; j < NBB; ++j) v |= (uint32_t)sstage[wave][r * nblk + b0 + j] << (8 * j);
+                    da.s[r] = v;
+                }
+            }
+            float part[kRowsB];
+            float chain = 0.f;
+#pragma unroll
+            for (int r = 0; r < kRowsB; ++r) {
+                float sum = 0.f;
+#pragma unroll
+                for (int j = 0; j < NBB; ++j) {
+                    reg_barrier_after(da.w[r][j], chain);
+                    sum = fmaf(fp4_block_dot(da.w[r][j], ms[j]), scale_of(da.s[r], j), sum);
+                    chain = sum;
+                }
+                part[r] = sum;
+                if (r + BD < kRowsB) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_row(r + BD);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            wave_reduce_n<kRowsB>(part, lane);
+            const int r = reduced_index<kRowsB>(lane);
+            if (valid && reduced_owner<kRowsB>(lane) && o0 + r < a.out_dim) acc[wave][0][r] += wt * part[0];
+        }
+    } else if (!PIPE) {
 #pragma unroll 1
         for (; u < U; u += kWavesB) {
             load_rows(u, da);
@@ -590,6 +740,7 @@ struct RouteTables {
     int32_t* off;               // [max_unique + 1] pair offsets per slot
     int32_t* pair_tok;          // [T*topk] token of each pair, grouped by slot
     float* pair_w;              // [T*topk] routing weight of each pair
+    int n_slots;                // entries of uexp; those past U are set to expert 0
 };
 
 // Top-k of one token's logits on one wave: descending, ties to the lower
@@ -760,6 +911,13 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
         rt.header[1] = P;
         rt.off[U] = P;
     }
+    {
+        // Slots past the routed ones get a valid expert id, so the one-token
+        // kernels may form weight addresses from any slot before checking it.
+        int total = 0;
+        for (int w = 0; w < kRouteThreads / 64; ++w) total += scan[w];
+        for (int u = (total >> 16) + tid; u < rt.n_slots; u += kRouteThreads) rt.uexp[u] = 0;
+    }
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kEntries; ++q) {
@@ -806,7 +964,7 @@ int env_int(const char* name, int def) {
 struct Shapes {
     int hc, pipe, h_per_wave;
     int rb, wb, bpipe;
-    int t1, t1_waves, t1_xfirst;
+    int t1, t1_waves, b1_depth;
 };
 
 const Shapes& shapes() {
@@ -820,12 +978,14 @@ const Shapes& shapes() {
         v.rb = (b / 100) >= 16 ? 16 : 8;
         v.wb = ((b / 10) % 10) >= 8 ? 8 : 4;
         v.bpipe = b % 10 == 1;
-        // One-token stage A: DSV4_GROUPED_T1 = waves*10 + xfirst (0 disables).
-        const int t1 = env_int("DSV4_GROUPED_T1", 41);
-        v.t1 = t1 >= 10;
-        v.t1_waves = t1 / 10 >= 16 ? 16 : (t1 / 10 >= 8 ? 8 : 4);
-        v.t1_xfirst = t1 % 10 == 1;
+        // One-token stage A: DSV4_GROUPED_T1 = waves per workgroup (4, 8, 16;
+        // "0" selects the generic kernel).
+        const int t1 = env_int("DSV4_GROUPED_T1", 4);
+        v.t1 = 1;
+        v.t1_waves = t1 >= 16 ? 16 : (t1 >= 8 ? 8 : 4);
         if (std::getenv("DSV4_GROUPED_T1") && std::atoi(std::getenv("DSV4_GROUPED_T1")) == 0) v.t1 = 0;
+        // Rows in flight before the first dot of one-token stage B (of 8).
+        v.b1_depth = env_int("DSV4_GROUPED_B1_DEPTH", 8);
         return v;
     }();
     return s;
@@ -861,18 +1021,19 @@ hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream) {
     dim3 block(64 * kWavesA);
 #define DSV4_A(NBV, HCV, FASTV, PIPEV) \
     hipLaunchKernelGGL((moe_swiglu_kernel<NBV, HCV, INDEXED, FASTV, PIPEV, MULTI>), grid, block, 0, stream, a)
-    if (fast && !MULTI && !pipe && sh.t1) {
-        const int W = sh.t1_waves;
-        dim3 g1((unsigned)((a.hidden + W * hc - 1) / (W * hc)), (unsigned)slots);
-#define DSV4_T1(NBV, HCV, WV, XF) \
-    hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, HCV, INDEXED, WV, XF>), g1, dim3(64 * WV), 0, stream, a)
-        if (nb == 1) DSV4_T1(1, 4, 4, true);
-        else if (W == 4 && sh.t1_xfirst) DSV4_T1(2, 4, 4, true);
-        else if (W == 4) DSV4_T1(2, 4, 4, false);
-        else if (W == 8 && sh.t1_xfirst) DSV4_T1(2, 4, 8, true);
-        else if (W == 8) DSV4_T1(2, 4, 8, false);
-        else if (sh.t1_xfirst) DSV4_T1(2, 4, 16, true);
-        else DSV4_T1(2, 4, 16, false);
+    // The one-token kernel takes whole tiles of W*4 rows and reads each
+    // tile's scales with 16-byte loads.
+    const int W = nb == 1 ? 4 : sh.t1_waves;
+    const bool t1 = fast && !MULTI && !pipe && sh.t1 && a.hidden % (W * 4) == 0 &&
+                    aligned16(a.s1) && aligned16(a.s3);
+    if (t1) {
+        dim3 g1((unsigned)(a.hidden / (W * 4)), (unsigned)slots);
+#define DSV4_T1(NBV, WV) \
+    hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4>), g1, dim3(64 * WV), 0, stream, a)
+        if (nb == 1) DSV4_T1(1, 4);
+        else if (W == 4) DSV4_T1(2, 4);
+        else if (W == 8) DSV4_T1(2, 8);
+        else DSV4_T1(2, 16);
 #undef DSV4_T1
     } else if (!fast) {
         if (nb == 1) DSV4_A(1, 2, false, false);
@@ -898,8 +1059,14 @@ hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
     const int nb = blocks_per_lane(a.hidden);
     a.scale_vec = scale_vec_ok(nb, a.hidden / kBlkElems, a.s2, a.s2);
     const bool fast = ALIGNED && a.hidden == 2048 * nb && (nb == 1 || a.scale_vec);
+    // Whole row tiles (RB divides 16) and 16-byte aligned scales: the
+    // one-token path stages each wave's scale rows with one load per lane.
+    a.stage_scales = !MULTI && a.out_dim % 16 == 0 && aligned16(a.s2);
 #define DSV4_B(NBV, RBV, WBV, FASTV, PIPEV)                                                        \
     hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, FASTV, PIPEV, MULTI>),       \
+                       dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
+#define DSV4_BD(NBV, RBV, WBV, BDV)                                                                \
+    hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, true, false, MULTI, BDV>),   \
                        dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
     if (!fast) {
         if (nb == 1) DSV4_B(1, 8, 4, false, false);
@@ -915,12 +1082,18 @@ hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
             case 881: DSV4_B(1, 8, 8, true, true); break;
             case 1640: DSV4_B(1, 16, 4, true, false); break;
             case 1680: DSV4_B(1, 16, 8, true, false); break;
-            default: DSV4_B(1, 8, 8, true, false); break;
+            default:
+                if (MULTI || sh.b1_depth >= 8) DSV4_B(1, 8, 8, true, false);
+                else if (sh.b1_depth >= 6) DSV4_BD(1, 8, 8, 6);
+                else if (sh.b1_depth >= 4) DSV4_BD(1, 8, 8, 4);
+                else DSV4_BD(1, 8, 8, 2);
+                break;
         }
     } else {
         return hipErrorInvalidValue;
     }
 #undef DSV4_B
+#undef DSV4_BD
     return hipGetLastError();
 }
 
@@ -981,6 +1154,9 @@ MoeCall moe_call(int T, int topk, int n_experts, int hidden, void* workspace) {
     c.es.pair_w = c.rt.pair_w;
     const int P = T * topk;
     c.es.n_slots = n_experts < P ? n_experts : P;
+    c.es.n_pairs = P;
+    c.es.n_experts = n_experts;
+    c.rt.n_slots = c.es.n_slots;
     return c;
 }
 
@@ -1105,6 +1281,8 @@ extern "C" int mxfp4_grouped_gemv_topk(const dsv4_bf16_t* x, const uint8_t* W1_p
     ExpertSet es{};
     es.rweights = rweights;
     es.n_slots = n_exp;
+    es.n_pairs = n_exp;
+    es.n_experts = n_exp;
 
     StageAArgs A{};
     A.x = reinterpret_cast<const uint16_t*>(x);
