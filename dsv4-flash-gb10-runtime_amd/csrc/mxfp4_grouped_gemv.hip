@@ -70,18 +70,19 @@ struct ExpertSet {
     int n_experts;              // experts of the per-layer tensors (indexed)
 };
 
-// Slot u of a one-pair-per-slot launch (T == 1), with every table read
-// unconditional and independent, so the weight loads that depend on the
-// expert id are issued after a single round trip. Tables past the routed
-// slots hold valid ids (the routing kernel fills them), and the ids and pair
-// index are clamped into range anyway; `valid` says whether the slot is routed.
+// Slot u of a one-token launch (T == 1), with every table read unconditional
+// and independent, so the weight loads that depend on the expert id are
+// issued after a single round trip. With one token every routed expert serves
+// exactly one pair and pairs are grouped by slot, so slot u's pair is pair u.
+// Tables past the routed slots hold valid ids (the routing kernel fills them)
+// and ids are clamped into range anyway; `valid` says whether u is routed.
 template <bool INDEXED>
 __device__ __forceinline__ void slot_info_t1(const ExpertSet& s, int u, int& expert, int& pbeg,
                                              float& w, bool& valid) {
     if constexpr (INDEXED) {
         const int U = *s.n_unique;
         expert = min(max(s.uexp[u], 0), s.n_experts - 1);
-        pbeg = min(max(s.off[u], 0), s.n_pairs - 1);
+        pbeg = min(u, s.n_pairs - 1);
         w = s.pair_w[pbeg];
         valid = u < U;
     } else {
@@ -90,6 +91,32 @@ __device__ __forceinline__ void slot_info_t1(const ExpertSet& s, int u, int& exp
         w = s.rweights[u];
         valid = u < s.n_slots;
     }
+}
+
+// slot_info_t1 for slot `u` (wave-uniform) read by all lanes at once: lane l
+// loads slot min(l, n_slots-1)'s entries (one round trip, no load depending
+// on another) and the wave's slot is broadcast from lane u.
+template <bool INDEXED>
+__device__ __forceinline__ void slot_info_t1_wave(const ExpertSet& s, int u, int lane, int& expert,
+                                                  int& pbeg, float& w, bool& valid) {
+    const int t = min(lane, s.n_slots - 1);
+    int e_l;
+    float w_l;
+    int U;
+    if constexpr (INDEXED) {
+        U = *s.n_unique;
+        e_l = s.uexp[t];
+        w_l = s.pair_w[min(t, s.n_pairs - 1)];
+    } else {
+        U = s.n_slots;
+        e_l = t;
+        w_l = s.rweights[t];
+    }
+    expert = __builtin_amdgcn_readlane(e_l, u);
+    w = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w_l), u));
+    expert = INDEXED ? min(max(expert, 0), s.n_experts - 1) : expert;
+    pbeg = min(u, s.n_pairs - 1);
+    valid = u < U && u < s.n_slots;
 }
 
 template <bool INDEXED>
@@ -535,11 +562,16 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
     __shared__ float acc[kWavesB][TMAX][kRowsB];
     __shared__ __align__(16) uint8_t sstage[(!PIPE && !MULTI && FAST) ? kWavesB : 1][kRowsB * 64 * NBB];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar table loads
     const int o0 = blockIdx.x * kRowsB;
-    float* accf = &acc[0][0][0];
-    for (int i = threadIdx.x; i < kWavesB * TMAX * kRowsB; i += 64 * kWavesB) accf[i] = 0.f;
-    __syncthreads();
+    // The one-token path writes every acc[wave][0][r] itself; the others
+    // accumulate into zeroed slots.
+    const bool t1_path = !PIPE && !MULTI && FAST && a.stage_scales && a.es.n_slots <= kWavesB;
+    if (!t1_path) {
+        float* accf = &acc[0][0][0];
+        for (int i = threadIdx.x; i < kWavesB * TMAX * kRowsB; i += 64 * kWavesB) accf[i] = 0.f;
+        __syncthreads();
+    }
 
     int U;
     if constexpr (INDEXED) U = *a.es.n_unique;
@@ -623,77 +655,66 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
 
     DownRows<NBB, RB> da, db;
     int u = wave;
-    if (!PIPE && !MULTI && FAST) {
-        // One pair per slot (T == 1): the slot's M slice is loaded before its
-        // W2 rows, so the row dots start as soon as the first row arrives; the
-        // table reads are unconditional (slot_info_t1) and unrouted slots are
-        // computed but not accumulated.
-#pragma unroll 1
-        for (; u < a.es.n_slots; u += kWavesB) {
-            int expert, pbeg;
-            float wt;
-            bool valid;
-            slot_info_t1<INDEXED>(a.es, u, expert, pbeg, wt, valid);
-            uint32_t ms[NBB][16];
+    if (t1_path) {
+        // One token (host-checked: at most one slot per wave, whole 16-row
+        // tiles, 16-byte aligned scales). Wave w takes slot w: its table
+        // reads are unconditional (slot_info_t1); its M slice, then its
+        // kRowsB scale rows (one load of kRowsB*NBB bytes per lane, spread
+        // through the wave's LDS slot), then its W2 rows are issued, so the
+        // dots start as soon as the first row arrives. No branch surrounds a
+        // load, so every wait covers exactly the loads it needs.
+        int expert, pbeg;
+        float wt;
+        bool valid;
+        slot_info_t1_wave<INDEXED>(a.es, wave, lane, expert, pbeg, wt, valid);
+        uint32_t ms[NBB][16];
+#pragma unroll
+        for (int j = 0; j < NBB; ++j)
+            load_act_block<true>(a.M + (int64_t)pbeg * a.hidden + (b0 + j) * kBlkElems, ms[j]);
+        const uint8_t* W2 = a.w2 + (int64_t)expert * a.w_exp_stride;
+        const uint8_t* S2 = a.s2 + (int64_t)expert * a.s_exp_stride;
+        using SPiece = typename ScalePiece<kRowsB * NBB>::type;
+        const SPiece spiece =
+            *reinterpret_cast<const SPiece*>(S2 + (int64_t)o0 * nblk + lane * (kRowsB * NBB));
+        __builtin_amdgcn_sched_barrier(0);  // keep the M and scale loads oldest
+        auto load_row = [&](int r) {
+            const int o = min(o0 + r, a.out_dim - 1);
 #pragma unroll
             for (int j = 0; j < NBB; ++j)
-                load_act_block<true>(a.M + (int64_t)pbeg * a.hidden + (b0 + j) * kBlkElems, ms[j]);
-            __builtin_amdgcn_sched_barrier(0);  // keep the M loads oldest
-            const uint8_t* W2 = a.w2 + (int64_t)expert * a.w_exp_stride;
-            const uint8_t* S2 = a.s2 + (int64_t)expert * a.s_exp_stride;
-            // The wave's kRowsB scale rows (kRowsB * nblk contiguous bytes) in
-            // one load of kRowsB*NBB bytes per lane, instead of one small load
-            // per row; redistributed through the wave's LDS slot below.
-            using SPiece = typename ScalePiece<kRowsB * NBB>::type;
-            SPiece spiece{};
-            if (a.stage_scales)
-                spiece = *reinterpret_cast<const SPiece*>(S2 + (int64_t)o0 * nblk + lane * (kRowsB * NBB));
-            __builtin_amdgcn_sched_barrier(0);
-            auto load_row = [&](int r) {
-                const int o = min(o0 + r, a.out_dim - 1);
+                da.w[r][j] = ld16_stream(W2 + (int64_t)o * wrow + (int64_t)(b0 + j) * 16);
+        };
 #pragma unroll
-                for (int j = 0; j < NBB; ++j)
-                    da.w[r][j] = ld16_stream(W2 + (int64_t)o * wrow + (int64_t)(b0 + j) * 16);
-                if (!a.stage_scales) da.s[r] = load_scales<NBB>(S2 + (int64_t)o * nblk + b0, true, NBB);
-            };
-            // BD rows in flight before the first dot; row r+BD is issued after
-            // row r's dot.
+        for (int r = 0; r < BD; ++r) load_row(r);
+        reinterpret_cast<SPiece*>(&sstage[wave][0])[lane] = spiece;
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int r = 0; r < BD; ++r) load_row(r);
-            if (a.stage_scales) {
-                SPiece* slot = reinterpret_cast<SPiece*>(&sstage[wave][0]);
-                slot[lane] = spiece;
-                __builtin_amdgcn_wave_barrier();
+        for (int r = 0; r < kRowsB; ++r) {
+            uint32_t v = 0;
 #pragma unroll
-                for (int r = 0; r < kRowsB; ++r) {
-                    uint32_t v = 0;
-#pragma unroll
-                    for (int j = 0; j < NBB; ++j) v |= (uint32_t)sstage[wave][r * nblk + b0 + j] << (8 * j);
-                    da.s[r] = v;
-                }
-            }
-            float part[kRowsB];
-            float chain = 0.f;
-#pragma unroll
-            for (int r = 0; r < kRowsB; ++r) {
-                float sum = 0.f;
-#pragma unroll
-                for (int j = 0; j < NBB; ++j) {
-                    reg_barrier_after(da.w[r][j], chain);
-                    sum = fmaf(fp4_block_dot(da.w[r][j], ms[j]), scale_of(da.s[r], j), sum);
-                    chain = sum;
-                }
-                part[r] = sum;
-                if (r + BD < kRowsB) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    load_row(r + BD);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            wave_reduce_n<kRowsB>(part, lane);
-            const int r = reduced_index<kRowsB>(lane);
-            if (valid && reduced_owner<kRowsB>(lane) && o0 + r < a.out_dim) acc[wave][0][r] += wt * part[0];
+            for (int j = 0; j < NBB; ++j) v |= (uint32_t)sstage[wave][r * nblk + b0 + j] << (8 * j);
+            da.s[r] = v;
         }
+        float part[kRowsB];
+        float chain = 0.f;
+#pragma unroll
+        for (int r = 0; r < kRowsB; ++r) {
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < NBB; ++j) {
+                reg_barrier_after(da.w[r][j], chain);
+                sum = fmaf(fp4_block_dot(da.w[r][j], ms[j]), scale_of(da.s[r], j), sum);
+                chain = sum;
+            }
+            part[r] = sum;
+            if (r + BD < kRowsB) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_row(r + BD);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        wave_reduce_n<kRowsB>(part, lane);
+        const int r = reduced_index<kRowsB>(lane);
+        if (reduced_owner<kRowsB>(lane)) acc[wave][0][r] = valid ? wt * part[0] : 0.f;  // out_dim % 16 == 0
     } else if (!PIPE) {
 #pragma unroll 1
         for (; u < U; u += kWavesB) {
@@ -1059,9 +1080,10 @@ hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
     const int nb = blocks_per_lane(a.hidden);
     a.scale_vec = scale_vec_ok(nb, a.hidden / kBlkElems, a.s2, a.s2);
     const bool fast = ALIGNED && a.hidden == 2048 * nb && (nb == 1 || a.scale_vec);
-    // Whole row tiles (RB divides 16) and 16-byte aligned scales: the
-    // one-token path stages each wave's scale rows with one load per lane.
-    a.stage_scales = !MULTI && a.out_dim % 16 == 0 && aligned16(a.s2);
+    // The one-token path of the FAST kernels: whole row tiles (RB divides
+    // 16), 16-byte aligned scales (staged with one load per lane) and at most
+    // one expert slot per wave (8 waves).
+    a.stage_scales = !MULTI && a.out_dim % 16 == 0 && aligned16(a.s2) && a.es.n_slots <= 8;
 #define DSV4_B(NBV, RBV, WBV, FASTV, PIPEV)                                                        \
     hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, FASTV, PIPEV, MULTI>),       \
                        dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
