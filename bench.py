@@ -72,6 +72,114 @@ def profiled_traffic(kernel: str):
     return None, None
 
 
+MALL_DEFEAT_BYTES = 512 << 20   # rotate weight copies over >= 2x the 256 MB MALL
+
+
+def dense_kernels(torch, dev, cpu: bool) -> dict:
+    """The other three drop-in kernels at their BASELINE.json shapes: dense
+    MXFP4 GEMV, FP8-E4M3 GEMV (configs[2], T in {1, 8}) and
+    fused RMSNorm + residual (configs[1], T in {1, 8, 64}). Each case replays a
+    HIP graph of launches that rotate over enough weight copies (>= 512 MB) for
+    the weights to come from HBM; µs per launch, algorithmic GB/s and the
+    fraction of 8 TB/s are reported, with the CPU oracle's time for one call
+    beside it (cpu=True)."""
+    from oracle import mx  # CPU baseline only
+    from runtime import fp8_e4m3_gemv_binding as fp8b
+    from runtime import mxfp4_gemv_binding as mxb
+    from runtime import rmsnorm_fuse_binding as rb
+    from runtime import synth
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def u8(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.uint8)).to(dev)
+
+    def bf(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.uint16).view(np.int16)).view(torch.bfloat16).to(dev)
+
+    def rep(t, n):
+        return t.unsqueeze(0).repeat(n, *([1] * t.dim()))
+
+    def copies(t, nbytes_per_copy):
+        n = max(2, -(-MALL_DEFEAT_BYTES // nbytes_per_copy))
+        return rep(t, n), n
+
+    def time_launches(fn, n_copies, reps=4):
+        fn(0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        n = max(n_copies, 64)
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i % n_copies)
+        g.replay()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(reps):
+            g.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) * 1e3 / (reps * n)
+
+    def cpu_us(fn):
+        if not cpu:
+            return None
+        t0 = time.perf_counter()
+        fn()
+        return round((time.perf_counter() - t0) * 1e6, 1)
+
+    def entry(us, nbytes, cpu_time):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"us": round(us, 3), "algorithmic_bytes": int(nbytes), "gbs": round(gbs, 1),
+                "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "cpu_oracle_us": cpu_time}
+
+    out = {}
+    # configs[0]: MXFP4 dense 2048 x 4096
+    N0, K0 = 2048, 4096
+    p, s = synth.mxfp4_weight(1000, N0, K0)
+    x0 = synth.normal_bf16(1001, (K0,))
+    P, nP = copies(u8(p[0]), N0 * K0 // 2 + N0 * K0 // 32)
+    S = rep(u8(s[0]), nP)
+    xd = bf(x0)
+    y = torch.empty(N0, dtype=torch.bfloat16, device=dev)
+    us = time_launches(lambda i: mxb.mxfp4_gemv(P[i], S[i], xd, out=y), nP)
+    out["mxfp4_gemv_m1 2048x4096"] = entry(us, N0 * K0 // 2 + N0 * K0 // 32 + 2 * K0 + 2 * N0,
+                                            cpu_us(lambda: mx.mxfp4_gemv(x0, p[0], s[0])))
+    del P, S
+    # configs[2]: FP8 GEMVs, T in {1, 8}
+    for (N, K) in ((1536, 4096), (576, 4096), (4096, 4096), (4096, 2048)):
+        w, ws = synth.fp8_weight(1002 + N + K, N, K)
+        wbytes = N * K + ws.size
+        W, nW = copies(u8(w), wbytes)
+        WS = rep(u8(ws), nW)
+        for T in (1, 8):
+            xh = synth.normal_bf16(2002 + T, (T, K))
+            xd = bf(xh) if T > 1 else bf(xh[0])
+            y = torch.empty((T, N) if T > 1 else (N,), dtype=torch.bfloat16, device=dev)
+            us = time_launches(lambda i: fp8b.fp8_e4m3_gemv(W[i], WS[i], xd, out=y), nW)
+            out[f"fp8_e4m3_gemv {N}x{K} T={T}"] = entry(us, wbytes + T * (2 * K + 2 * N),
+                                                         cpu_us(lambda: mx.fp8_gemv(xh, w, ws)))
+        del W, WS
+    # configs[1]: RMSNorm + residual, H = 4096
+    H = 4096
+    g = synth.normal_bf16(1203, (H,), 1.0, 0.1)
+    gd = bf(g)
+    for T in (1, 8, 64):
+        h = synth.normal_bf16(1201 + T, (T, H))
+        r = synth.normal_bf16(1301 + T, (T, H), 0.0, 0.5)
+        nb = 4 * T * H * 2
+        Hc, nH = copies(bf(h), nb)
+        Rc = rep(bf(r), nH)
+        yo = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        ro = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        us = time_launches(lambda i: rb.rmsnorm_fuse_residual_add(Hc[i], Rc[i], gd, out_norm=yo,
+                                                                  out_new_residual=ro), nH)
+        out[f"rmsnorm_fuse_residual_add T={T}x{H}"] = entry(us, nb + 2 * H,
+                                                            cpu_us(lambda: mx.rmsnorm_residual(h, r, g)))
+        del Hc, Rc
+    return out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -91,6 +199,8 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=1, help="decode tokens per step (config 3: 1, 4, 16)")
     ap.add_argument("--layers", type=int, default=4, help="resident layers cycled over (MALL defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true",
+                    help="skip the dense MXFP4 / FP8 / RMSNorm per-kernel lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -248,6 +358,13 @@ def main() -> int:
         }
         del ids0
 
+    kernels = None
+    if not args.no_kernels:
+        del layers, mods
+        torch.cuda.empty_cache()
+        log("per-kernel lines: dense MXFP4, FP8, RMSNorm")
+        kernels = dense_kernels(torch, dev, cpu=not args.no_cpu_baseline)
+
     traffic, traffic_src = profiled_traffic(STAGE_A_KERNEL)
     result = {
         "metric": METRIC,
@@ -288,6 +405,7 @@ def main() -> int:
             "avg_launch_us": round(a_us, 3),
         },
         "cpu_baseline": cpu,
+        "kernels": kernels,
     }
     print(json.dumps(result), flush=True)
     return 0

@@ -123,6 +123,71 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
     }
 }
 
+// Tile kernel for K in {2048, 4096} with 16-byte aligned rows and
+// activations (the MLA projection shapes). A workgroup of 256 threads owns
+// R = C*256/KC rows (KC = K/16 chunks per row); thread t takes the chunks
+// t, t+256, ..., t+256*(C-1) of the workgroup's [R, KC] chunk grid, so all of
+// its chunks share one k-slice (k = 16*(t % KC)) and every wave instruction
+// reads 1 KiB of a single row. Each thread issues its activation slice for all
+// TT tokens first (16 bf16 per token), then its C weight chunks and their
+// tile-scale bytes, all unconditional (rows clamped, tokens past T clamped to
+// T-1 and not stored), so everything is in flight after one issue pass.
+// Per-wave partials (C x TT values, one butterfly) meet in LDS and are added
+// in a fixed order: deterministic.
+template <int C, int TT, int KC>
+__global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a) {
+    constexpr int kRowsWG = C * 256 / KC;
+    constexpr int kVals = C * TT;
+    __shared__ float part[kWaves][C][TT];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int n0 = blockIdx.x * kRowsWG;
+    const int k = 16 * (t % KC);
+
+    uint32_t xp[TT][8];
+#pragma unroll
+    for (int tok = 0; tok < TT; ++tok) {
+        const u32x4* s4 = reinterpret_cast<const u32x4*>(a.x + (int64_t)min(tok, a.T - 1) * a.xstride + k);
+        const u32x4 v0 = s4[0], v1 = s4[1];
+        xp[tok][0] = v0[0]; xp[tok][1] = v0[1]; xp[tok][2] = v0[2]; xp[tok][3] = v0[3];
+        xp[tok][4] = v1[0]; xp[tok][5] = v1[1]; xp[tok][6] = v1[2]; xp[tok][7] = v1[3];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // activation loads first
+    u32x4 w[C];
+    uint32_t sb[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const int n = min(n0 + (t + 256 * i) / KC, a.N - 1);
+        w[i] = ld16_stream(a.w + (int64_t)n * a.wrow + k);
+        sb[i] = a.s[(int64_t)(n / kTile) * a.srow + k / kTile];
+    }
+    float acc[kVals];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const float sc = e8m0_to_f32(sb[i]);
+#pragma unroll
+        for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[i], xp[tok]) * sc;
+    }
+    wave_reduce_n<kVals>(acc, lane);
+    const int v = reduced_index<kVals>(lane);
+    if (reduced_owner<kVals>(lane)) part[wave][v / TT][v % TT] = acc[0];
+    __syncthreads();
+    for (int o = t; o < kRowsWG * TT; o += 256) {
+        const int r = o / TT;
+        const int tok = o % TT;
+        if (tok >= a.T || n0 + r >= a.N) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if ((64 * w2 + 256 * i) / KC == r) sum += part[w2][i][tok];
+        }
+        a.y[(int64_t)tok * a.ystride + n0 + r] = f32_to_bf16_bits(sum);
+    }
+}
+
 // One thread per 16 bytes of a row.
 __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* w, const uint8_t* s, int K,
                                                           int N, int64_t wrow, int64_t srow,
@@ -167,6 +232,27 @@ int validate(int K, int N) {
 int launch(const Fp8Args& a, hipStream_t stream) {
     const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) &&
                     (a.T == 1 || a.xstride % 8 == 0);
+    if (al && (a.K == 2048 || a.K == 4096)) {
+        // Four chunks per thread: 4 rows per workgroup at K = 4096, 8 at 2048.
+        const int KC = a.K / 16;
+        const int rows = 4 * 256 / KC;
+        const dim3 grid((unsigned)((a.N + rows - 1) / rows));
+#define DSV4_TILE(TTV)                                                                            \
+    if (KC == 256) hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 256>), grid, dim3(256), 0, stream, a); \
+    else hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 128>), grid, dim3(256), 0, stream, a);
+        if (a.T == 1) { DSV4_TILE(1) }
+        else if (a.T == 2) { DSV4_TILE(2) }
+        else if (a.T <= 4) { DSV4_TILE(4) }
+        else if (a.T <= 8) { DSV4_TILE(8) }
+        else { DSV4_TILE(16) }
+#undef DSV4_TILE
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            std::fprintf(stderr, "fp8_e4m3_gemv launch failed: %s\n", hipGetErrorString(e));
+            return -4;
+        }
+        return 0;
+    }
     const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)));
     const dim3 block(64 * kWaves);
     const int nc = (a.K + 1023) / 1024;

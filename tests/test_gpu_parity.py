@@ -70,7 +70,7 @@ def test_fp8_dequant_exhaustive_bit_exact(device):
 # ------------------------------------------------------------- MXFP4 GEMV --
 
 @pytest.mark.parametrize("N,K", [(2048, 4096), (2047, 4096), (64, 32), (96, 96), (40, 2048),
-                                 (33, 8192), (128, 6144)])
+                                 (33, 8192), (128, 6144), (1, 4096), (13, 2048)])
 def test_mxfp4_gemv(device, N, K):
     announce(f"mxfp4_gemv_m1 N={N} K={K}")
     p, s = synth.mxfp4_weight(1000 + K, N, K)
@@ -131,6 +131,19 @@ def test_fp8_gemv_config_shapes(device, N, K, T):
     y = fp8b.fp8_e4m3_gemv(tw, ts, xt[0] if T == 1 else xt)
     ref = mx.fp8_gemv(x, w, s)
     assert_close(host_bits(y).reshape(T, N), ref, f"fp8 N={N} K={K} T={T}")
+
+
+@pytest.mark.parametrize("N,K,T", [(130, 4096, 2), (77, 2048, 5), (300, 4096, 16), (1, 2048, 1),
+                                   (9, 4096, 3)])
+def test_fp8_gemv_tile_path_tokens_and_ragged_n(device, N, K, T):
+    """The K in {2048, 4096} tile kernel: token counts padded to 2/4/8/16, rows
+    not a multiple of the workgroup tile."""
+    announce(f"fp8_e4m3_gemv tile N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(4100 + N + T, N, K)
+    x = synth.normal_bf16(4200 + T, (T, K))
+    xd = dev_bf16(x, device)
+    y = fp8b.fp8_e4m3_gemv(dev_u8(w, device), dev_u8(s, device), xd if T > 1 else xd[0])
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 tile N={N} K={K} T={T}")
 
 
 def test_fp8_gemv_long_rows_and_ragged_n(device):
