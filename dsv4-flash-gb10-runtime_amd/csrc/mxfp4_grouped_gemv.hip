@@ -196,7 +196,80 @@ __device__ __forceinline__ float scale_of(uint32_t packed, int j) {
     return e8m0_to_f32((packed >> (8 * j)) & 0xFFu);
 }
 
+// Top-k of one token's logits on one wave: descending, ties to the lower
+// expert index, weights sigmoid(l) renormalised to sum 1. Lane k < topk
+// returns the k-th pick. Each lane holds PER logits (expert lane + 64*i);
+// each round takes the wave maximum (DPP), then the lowest index holding it;
+// a picked entry becomes NaN, which fmaxf and the comparisons ignore. NaN
+// logits rank as -inf.
+template <int PER>
+__device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk,
+                                                  int lane, int& my_e, float& my_w) {
+    const float kRemoved = __uint_as_float(0x7FC00000u);
+    float v[PER];
+    // Unconditional loads (index clamped into the row) so all of them are in
+    // flight together; entries past n_experts become "removed".
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = lane + 64 * i;
+        float l = lt[min(e, n_experts - 1)];
+        l = (l != l) ? -INFINITY : l;
+        v[i] = e < n_experts ? l : kRemoved;
+    }
+    my_e = 0;
+    float my_l = -INFINITY;
+    for (int k = 0; k < topk; ++k) {
+        float best = v[0];
+#pragma unroll
+        for (int i = 1; i < PER; ++i) best = fmaxf(best, v[i]);
+        const float wmax = wave_max_f32(best);
+        int idx = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = PER - 1; i >= 0; --i)
+            if (v[i] == wmax) idx = lane + 64 * i;
+        idx = wave_min_i32(idx);
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (lane + 64 * i == idx) v[i] = kRemoved;
+        if (lane == k) {
+            my_e = idx;
+            my_l = wmax;
+        }
+    }
+    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
+    my_w = s / wave_sum_f32(s);
+}
+
+__device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int lane,
+                                              int& e, float& w) {
+    if (n_experts <= 256) wave_topk_sigmoid<4>(lt, n_experts, topk, lane, e, w);
+    else if (n_experts <= 512) wave_topk_sigmoid<8>(lt, n_experts, topk, lane, e, w);
+    else wave_topk_sigmoid<16>(lt, n_experts, topk, lane, e, w);
+}
+
 // ---------------------------------------------------------------- stage A --
+
+// Device routing tables of the expert-indexed path (in the workspace):
+struct RouteTables {
+    int32_t* header;            // [0] = unique experts U, [1] = pairs P
+    int32_t* uexp;              // [max_unique] expert id per slot, ascending
+    int32_t* off;               // [max_unique + 1] pair offsets per slot
+    int32_t* pair_tok;          // [T*topk] token of each pair, grouped by slot
+    float* pair_w;              // [T*topk] routing weight of each pair
+    int n_slots;                // entries of uexp; those past U are set to expert 0
+};
+
+// One-token gating folded into stage A (mxfp4_moe_layer at T = 1): every
+// workgroup computes the top-k of the logits itself and workgroup (0, 0)
+// publishes ids, weights and the routing tables stage B reads.
+struct GateArgs {
+    const float* logits;        // [n_experts] fp32
+    int n_experts;
+    int topk;
+    int32_t* ids_out;           // [topk] or null
+    float* w_out;               // [topk] or null
+    RouteTables rt;
+};
 
 struct StageAArgs {
     const uint16_t* x;          // [T, K] bf16
@@ -212,6 +285,7 @@ struct StageAArgs {
     int scale_vec;              // scale rows allow NB-byte vector loads
     uint16_t* M;                // [pairs, hidden] bf16
     ExpertSet es;
+    GateArgs gate;
 };
 
 // HC hidden rows of W1 and of W3 in registers: NB 16-byte blocks per lane per
@@ -395,7 +469,7 @@ __global__ __launch_bounds__(64 * kWavesA, PIPE ? 1 : 4) void moe_swiglu_kernel(
 // only then writes activation and scales to LDS: the wait covers the oldest
 // loads only, so the weight stream starts at once. Rows past `hidden` and
 // unrouted slots are loaded but not stored.
-template <int NB, int HC, bool INDEXED, int kT1Waves, int D>
+template <int NB, int HC, bool INDEXED, int kT1Waves, int D, bool GATE>
 __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const StageAArgs a) {
     constexpr int kThreads = 64 * kT1Waves;
     constexpr int kRows = kT1Waves * HC;
@@ -404,38 +478,72 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     constexpr int kSPer = (kSTile / 16 + kThreads - 1) / kThreads;     // 16-byte scale pieces per thread
     __shared__ u32x4 xl[kMaxRed * 2 / 16];
     __shared__ u32x4 sl[kSTile / 16];
+    __shared__ int s_pick[GATE ? kMaxTopk : 1];
     const uint8_t* slb = reinterpret_cast<const uint8_t*>(sl);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    int expert, pbeg;
-    float wt;
-    bool valid;
-    slot_info_t1<INDEXED>(a.es, blockIdx.y, expert, pbeg, wt, valid);
-    (void)wt;
     const int hw = blockIdx.x * kRows;        // first row of the workgroup (hidden % kRows == 0)
     const int h0 = hw + wave * HC;
     const int K = a.K;
     const int nblk = K / kBlkElems;
     const int64_t wrow = K / 2;
-    const uint8_t* W1 = a.w1 + (int64_t)expert * a.w_exp_stride;
-    const uint8_t* W3 = a.w3 + (int64_t)expert * a.w_exp_stride;
-    const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
-    const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
 
     const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);  // token 0
     const int nx = K / 8;
     const int ns = kRows * nblk / 16;                        // 16-byte scale pieces per matrix
     u32x4 xv[kXPer];
-    u32x4 sv[kSPer];
 #pragma unroll
     for (int i = 0; i < kXPer; ++i) xv[i] = xg[min((int)threadIdx.x + kThreads * i, nx - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // the activation loads go first
+
+    int expert, pbeg;
+    bool valid;
+    if constexpr (GATE) {
+        // Wave 0 ranks the logits (the same computation in every workgroup);
+        // workgroup (0, 0) publishes the routing for stage B and the caller.
+        if (wave == 0) {
+            const GateArgs& g = a.gate;
+            int e;
+            float w;
+            wave_topk_any(g.logits, g.n_experts, g.topk, lane, e, w);
+            if (lane < g.topk) s_pick[lane] = e;
+            if (blockIdx.x == 0 && blockIdx.y == 0 && lane < g.topk) {
+                if (g.ids_out != nullptr) {
+                    g.ids_out[lane] = e;
+                    g.w_out[lane] = w;
+                }
+                g.rt.uexp[lane] = e;
+                g.rt.off[lane] = lane;
+                g.rt.pair_tok[lane] = 0;
+                g.rt.pair_w[lane] = w;
+                if (lane == 0) {
+                    g.rt.header[0] = g.topk;
+                    g.rt.header[1] = g.topk;
+                    g.rt.off[g.topk] = g.topk;
+                }
+            }
+        }
+        __syncthreads();
+        expert = s_pick[blockIdx.y];
+        pbeg = blockIdx.y;
+        valid = true;
+    } else {
+        float wt;
+        slot_info_t1<INDEXED>(a.es, blockIdx.y, expert, pbeg, wt, valid);
+        (void)wt;
+    }
+    const uint8_t* W1 = a.w1 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* W3 = a.w3 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
+    const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
+    u32x4 sv[kSPer];
 #pragma unroll
     for (int i = 0; i < kSPer; ++i) {
         const int t = min((int)threadIdx.x + kThreads * i, 2 * ns - 1);
         const uint8_t* src = t < ns ? S1 + 16 * t : S3 + 16 * (t - ns);
         sv[i] = *reinterpret_cast<const u32x4*>(src);
     }
-    __builtin_amdgcn_sched_barrier(0);  // keep the activation and scale loads oldest
+    __builtin_amdgcn_sched_barrier(0);  // then the scale tile, then the weights
 
     GateUpChunk<NB, HC> c;
     auto load_row = [&](int r) {
@@ -754,66 +862,6 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
 
 // ------------------------------------------------------------ routing ------
 
-// Device routing tables of the expert-indexed path (in the workspace):
-struct RouteTables {
-    int32_t* header;            // [0] = unique experts U, [1] = pairs P
-    int32_t* uexp;              // [max_unique] expert id per slot, ascending
-    int32_t* off;               // [max_unique + 1] pair offsets per slot
-    int32_t* pair_tok;          // [T*topk] token of each pair, grouped by slot
-    float* pair_w;              // [T*topk] routing weight of each pair
-    int n_slots;                // entries of uexp; those past U are set to expert 0
-};
-
-// Top-k of one token's logits on one wave: descending, ties to the lower
-// expert index, weights sigmoid(l) renormalised to sum 1. Lane k < topk
-// returns the k-th pick. Each lane holds PER logits (expert lane + 64*i);
-// each round takes the wave maximum (DPP), then the lowest index holding it;
-// a picked entry becomes NaN, which fmaxf and the comparisons ignore. NaN
-// logits rank as -inf.
-template <int PER>
-__device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk,
-                                                  int lane, int& my_e, float& my_w) {
-    const float kRemoved = __uint_as_float(0x7FC00000u);
-    float v[PER];
-    // Unconditional loads (index clamped into the row) so all of them are in
-    // flight together; entries past n_experts become "removed".
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        float l = lt[min(e, n_experts - 1)];
-        l = (l != l) ? -INFINITY : l;
-        v[i] = e < n_experts ? l : kRemoved;
-    }
-    my_e = 0;
-    float my_l = -INFINITY;
-    for (int k = 0; k < topk; ++k) {
-        float best = v[0];
-#pragma unroll
-        for (int i = 1; i < PER; ++i) best = fmaxf(best, v[i]);
-        const float wmax = wave_max_f32(best);
-        int idx = 0x7FFFFFFF;
-#pragma unroll
-        for (int i = PER - 1; i >= 0; --i)
-            if (v[i] == wmax) idx = lane + 64 * i;
-        idx = wave_min_i32(idx);
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (lane + 64 * i == idx) v[i] = kRemoved;
-        if (lane == k) {
-            my_e = idx;
-            my_l = wmax;
-        }
-    }
-    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
-    my_w = s / wave_sum_f32(s);
-}
-
-__device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int lane,
-                                              int& e, float& w) {
-    if (n_experts <= 256) wave_topk_sigmoid<4>(lt, n_experts, topk, lane, e, w);
-    else if (n_experts <= 512) wave_topk_sigmoid<8>(lt, n_experts, topk, lane, e, w);
-    else wave_topk_sigmoid<16>(lt, n_experts, topk, lane, e, w);
-}
 
 constexpr int kRouteThreads = 256;
 constexpr int kExpPerThread = kMaxExperts / kRouteThreads;  // 4
@@ -1028,8 +1076,21 @@ int scale_vec_ok(int nb, int nblk, const void* s0, const void* s1) {
 // FAST kernels: 16-byte aligned operands, every lane owning NB whole blocks of
 // every row (K == 2048*NB) and NB-byte scale loads; other shapes take the
 // checked path (HC = 2, one chunk per wave).
+//
+// Whether stage A of a one-token launch takes moe_swiglu_t1_kernel (16-byte
+// aligned operands, K = 2048 or 4096, whole row tiles, aligned scale rows).
+bool stage_a_t1_ok(const StageAArgs& a, bool aligned) {
+    const Shapes& sh = shapes();
+    const int nb = blocks_per_lane(a.K);
+    const bool fast = aligned && a.K == 2048 * nb && (nb == 1 || scale_vec_ok(nb, a.K / kBlkElems, a.s1, a.s3));
+    const int W = nb == 1 ? 4 : sh.t1_waves;
+    return fast && nb <= 2 && !sh.pipe && sh.t1 && a.hidden % (W * 4) == 0 && aligned16(a.s1) &&
+           aligned16(a.s3);
+}
+
+// gate: the one-token kernel also ranks a.gate.logits (requires stage_a_t1_ok).
 template <bool INDEXED, bool ALIGNED, bool MULTI>
-hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream) {
+hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, bool gate = false) {
     const Shapes& sh = shapes();
     const int nb = blocks_per_lane(a.K);
     a.scale_vec = scale_vec_ok(nb, a.K / kBlkElems, a.s1, a.s3);
@@ -1045,16 +1106,18 @@ hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream) {
     // The one-token kernel takes whole tiles of W*4 rows and reads each
     // tile's scales with 16-byte loads.
     const int W = nb == 1 ? 4 : sh.t1_waves;
-    const bool t1 = fast && !MULTI && !pipe && sh.t1 && a.hidden % (W * 4) == 0 &&
-                    aligned16(a.s1) && aligned16(a.s3);
+    const bool t1 = !MULTI && stage_a_t1_ok(a, ALIGNED);
+    if (gate && !(t1 && INDEXED)) return hipErrorInvalidValue;
     if (t1) {
         dim3 g1((unsigned)(a.hidden / (W * 4)), (unsigned)slots);
-#define DSV4_T1(NBV, WV) \
-    hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4>), g1, dim3(64 * WV), 0, stream, a)
-        if (nb == 1) DSV4_T1(1, 4);
-        else if (W == 4) DSV4_T1(2, 4);
-        else if (W == 8) DSV4_T1(2, 8);
-        else DSV4_T1(2, 16);
+#define DSV4_T1(NBV, WV)                                                                                       \
+    if (gate) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED>), g1, dim3(64 * WV), 0, \
+                                 stream, a);                                                                   \
+    else hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, false>), g1, dim3(64 * WV), 0, stream, a);
+        if (nb == 1) { DSV4_T1(1, 4) }
+        else if (W == 4) { DSV4_T1(2, 4) }
+        else if (W == 8) { DSV4_T1(2, 8) }
+        else { DSV4_T1(2, 16) }
 #undef DSV4_T1
     } else if (!fast) {
         if (nb == 1) DSV4_A(1, 2, false, false);
@@ -1197,7 +1260,7 @@ int launch_route(const float* logits, const int32_t* ids, const float* weights, 
 
 int launch_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed, const uint8_t* W3_packed,
                   const uint8_t* W1_scale, const uint8_t* W3_scale, int K_in, int hidden, int T,
-                  const MoeCall& c, hipStream_t stream) {
+                  const MoeCall& c, hipStream_t stream, const GateArgs* gate = nullptr) {
     StageAArgs A{};
     A.x = reinterpret_cast<const uint16_t*>(x);
     A.w1 = W1_packed;
@@ -1212,7 +1275,10 @@ int launch_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed, const uint8_t*
     A.es = c.es;
     const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
     hipError_t e;
-    if (T == 1)
+    if (gate != nullptr) {
+        A.gate = *gate;
+        e = launch_stage_a<true, true, false>(A, c.es.n_slots, stream, true);
+    } else if (T == 1)
         e = al ? launch_stage_a<true, true, false>(A, c.es.n_slots, stream)
                : launch_stage_a<true, false, false>(A, c.es.n_slots, stream);
     else
@@ -1426,6 +1492,21 @@ extern "C" int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
     if (v != 0) return v;
     if (topk > n_experts) return -4;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
+    if (T == 1 && (ids_out == nullptr) == (weights_out == nullptr)) {
+        // One token: the gating runs inside stage A (two launches in all).
+        StageAArgs probe{};
+        probe.K = K_in;
+        probe.hidden = hidden;
+        probe.s1 = W1_scale;
+        probe.s3 = W3_scale;
+        const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
+        if (stage_a_t1_ok(probe, al)) {
+            GateArgs g{logits, n_experts, topk, ids_out, weights_out, c.rt};
+            v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
+            if (v != 0) return v;
+            return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+        }
+    }
     v = launch_route(logits, nullptr, nullptr, T, topk, n_experts, ids_out, weights_out, c, stream);
     if (v != 0) return v;
     v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);

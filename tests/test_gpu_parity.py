@@ -373,13 +373,15 @@ def test_rmsnorm_scalar_path_and_noop(device):
 
 # ------------------------------------------------------------- HIP graphs ---
 
-def test_moe_layer_graph_replays_match_eager(device):
+@pytest.mark.parametrize("T,K", [(2, 1024), (1, 2048)])
+def test_moe_layer_graph_replays_match_eager(device, T, K):
     """A captured decode layer (gating + stages A/B, no memsets) replays
-    bit-identically to the eager call, with eager work between replays."""
+    bit-identically to the eager call, with eager work between replays. T = 1
+    at K = 2048 takes the path with the gating inside stage A."""
     from runtime import moe
 
-    E, K, H, O, T = 32, 1024, 512, 1024, 2
-    announce(f"mxfp4_moe_layer graph capture T={T} E={E}")
+    E, H, O = 32, 512, 1024
+    announce(f"mxfp4_moe_layer graph capture T={T} K={K} E={E}")
     weights = moe.make_moe_weights(9700, E, K, H, O, device)
     layer = moe.RoutedMoELayer(weights, topk=8, max_tokens=4)
     x = dev_bf16(synth.normal_bf16(9701, (T, K)), device)
