@@ -1,0 +1,459 @@
+// mxfp4_moe_prefill.hip — routed MXFP4 SwiGLU MoE for a prefill chunk (many
+// tokens) on the gfx950 matrix cores.
+//
+// Same result as the decode path (reference runtime/dsv4_engine_mxfp4.py:
+// 372-423 applied to every token):
+//   out[t] = bf16( sum_k w[t,k] * W2_e . bf16( silu(W1_e x_t) * (W3_e x_t) ) ),  e = ids[t,k]
+// For hundreds of tokens the expert products are real GEMMs, so they run on
+// v_mfma_f32_16x16x32_bf16. The MXFP4 weights are dequantised exactly to bf16
+// in registers (v_cvt_scalef32_pk_bf16_fp4 with the block's E8M0 scale: every
+// code * 2^e is a bf16 value) and the activations stay bf16, so the products
+// are exact and the sums are fp32, as on the VALU decode path.
+//
+// Launches (one stream, caller's workspace, no allocation, no atomics on
+// results):
+//   1. routing: pairs (token, k) grouped by expert, 64-token tiles per expert;
+//   2. stage A: per (tile, 64 hidden rows) M[pair, h] = bf16(silu(g) * u);
+//   3. stage B: per (tile, 64 output rows) Y[pair, o] = w * (W2_e . M[pair]) in fp32;
+//   4. combine: out[t, o] = bf16( sum_k Y[pos(t, k), o] ), k in order.
+// Each pair's row is computed independently of the other tokens of its tile,
+// so results do not depend on the order of pairs inside an expert.
+//
+// MFMA tiling: a workgroup (4 waves) owns 64 weight rows x up to 64 tokens of
+// one expert; wave w computes rows 16w..16w+15 against 4 token blocks of 16.
+// K advances in super-steps of 128 (4 MX blocks): lane l takes row l%16 and
+// MX block 4s + l/16 of the super-step, so its 16-byte load is one whole
+// block with one scale byte; k-step j (of 4) of the super-step uses elements
+// 8j..8j+7 of every lane's block, and the activation operand is read from an
+// LDS tile with the same k order. The next super-step's weights and
+// activation tile are loaded while the current one is multiplied.
+
+#include <cstdio>
+
+#include "dsv4_device.h"
+#include "dsv4_kernels.h"
+
+namespace {
+
+using namespace dsv4;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlk = 32;             // MX block
+constexpr int kTileTok = 64;         // tokens per tile
+constexpr int kTileRows = 64;        // weight rows per workgroup
+constexpr int kStep = 128;           // K per super-step
+constexpr int kLdsRow = kStep + 8;   // padded bf16 row of the activation tile (272 B)
+constexpr int kMaxTokens = 16384;
+constexpr int kMaxTopk = 16;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxRed = 8192;
+constexpr int kRouteThreads = 1024;
+
+struct PrefillTables {
+    int32_t* header;     // [0] tiles, [1] routed pairs
+    int32_t* pair_tok;   // [P] token of each pair, grouped by expert
+    float* pair_w;       // [P] routing weight of each pair
+    int32_t* pos;        // [P] pair index of entry (t, k), -1 if its id is out of range
+    int32_t* tile_e;     // [max_tiles] expert of each tile
+    int32_t* tile_p0;    // [max_tiles] first pair of each tile
+    int32_t* tile_n;     // [max_tiles] pairs in each tile (1..64)
+};
+
+// ------------------------------------------------------------- routing ----
+
+// Inclusive scan of one value per thread over a 1024-thread workgroup.
+__device__ __forceinline__ int block_scan(int v, int* wtot) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int up = __shfl_up(v, d, 64);
+        if (lane >= d) v += up;
+    }
+    if (lane == 63) wtot[wave] = v;
+    __syncthreads();
+    int add = 0;
+    for (int w = 0; w < wave; ++w) add += wtot[w];
+    __syncthreads();
+    return v + add;
+}
+
+// One workgroup: count the pairs of each expert (LDS atomics give each pair a
+// slot inside its expert), scan counts and tile counts, then write the pair
+// lists, the (t, k) -> pair map and the tile list. Pair order inside an
+// expert may vary between runs; results do not depend on it.
+__global__ __launch_bounds__(kRouteThreads) void prefill_route_kernel(const int32_t* ids,
+                                                                      const float* w, int P,
+                                                                      int topk, int n_experts,
+                                                                      PrefillTables pt) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int off[kMaxExperts];
+    __shared__ int toff[kMaxExperts];
+    __shared__ int wtot[kRouteThreads / 64];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < kMaxExperts; e += kRouteThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < P; i += kRouteThreads) {
+        const int e = ids[i];
+        pt.pos[i] = (e >= 0 && e < n_experts) ? atomicAdd(&cnt[e], 1) : -1;  // slot inside e
+    }
+    __syncthreads();
+    const int c = tid < n_experts ? cnt[tid] : 0;
+    const int nt = (c + kTileTok - 1) / kTileTok;
+    const int ci = block_scan(c, wtot);
+    const int ti = block_scan(nt, wtot);
+    if (tid < n_experts) {
+        off[tid] = ci - c;
+        toff[tid] = ti - nt;
+    }
+    if (tid == kRouteThreads - 1) {
+        pt.header[0] = ti;
+        pt.header[1] = ci;
+    }
+    __syncthreads();
+    for (int i = tid; i < P; i += kRouteThreads) {
+        const int e = ids[i];
+        const int slot = pt.pos[i];
+        if (slot >= 0) {
+            const int p = off[e] + slot;
+            pt.pair_tok[p] = i / topk;
+            pt.pair_w[p] = w[i];
+            pt.pos[i] = p;
+        }
+    }
+    if (tid < n_experts) {
+        for (int j = 0; j < nt; ++j) {
+            const int t = toff[tid] + j;
+            pt.tile_e[t] = tid;
+            pt.tile_p0[t] = off[tid] + kTileTok * j;
+            pt.tile_n[t] = min(kTileTok, c - kTileTok * j);
+        }
+    }
+}
+
+// --------------------------------------------------------------- GEMMs ----
+
+struct GemmArgs {
+    const uint16_t* act;        // activation rows: x [T, K] (stage A) or M [P, H] (stage B)
+    int64_t act_stride;         // elements between rows
+    int act_by_token;           // 1: act row = pair_tok[p] (stage A); 0: act row = p (stage B)
+    const uint8_t* wa;          // first weight matrix (W1 or W2), expert-major
+    const uint8_t* sa;
+    const uint8_t* wb;          // second weight matrix (W3) or null
+    const uint8_t* sb;
+    int64_t w_exp_stride;       // bytes per expert (packed)
+    int64_t s_exp_stride;
+    int K;                      // reduction length
+    int rows;                   // weight rows per expert (H or O)
+    const int32_t* header;
+    const int32_t* tile_e;
+    const int32_t* tile_p0;
+    const int32_t* tile_n;
+    const int32_t* pair_tok;
+    const float* pair_w;
+    uint16_t* M;                // stage A output [P, H] bf16
+    float* Y;                   // stage B output [P, O] fp32
+};
+
+// 16 bytes of e2m1 codes (one MX block) -> 32 bf16 in 4 operands of 8
+// (elements 8j..8j+7 in op[j]), times the block scale 2^(s-127) applied by
+// the conversion itself (exact). Scale byte 0xFF decodes to 0.
+__device__ __forceinline__ void dequant_block(u32x4 w, uint32_t s, bf16x8* op) {
+    const bool nan_scale = s == 0xFFu;
+    const float scale = __uint_as_float(nan_scale ? 0x3F800000u : (s << 23));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t d = nan_scale ? 0u : w[q];
+        const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
+        const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
+        const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
+        const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3);
+        bf16x8 v;
+        v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
+        v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
+        op[q] = v;
+    }
+}
+
+// grid = (max_tiles, rows / 64), block = 256. TWO: stage A (W1 and W3, SwiGLU
+// epilogue into M); otherwise stage B (W2, weighted fp32 rows into Y).
+template <bool TWO>
+__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) {
+    __shared__ __align__(16) uint16_t xs[2][kTileTok * kLdsRow];   // 2 x 17 KB
+    __shared__ int s_row[kTileTok];
+    const int ti = blockIdx.x;
+    if (ti >= a.header[0]) return;                                  // whole workgroup
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int e = a.tile_e[ti];
+    const int p0 = a.tile_p0[ti];
+    const int n = a.tile_n[ti];
+    const int nblk_tok = (n + 15) / 16;
+    if (t < kTileTok) {
+        const int p = p0 + min(t, n - 1);
+        s_row[t] = a.act_by_token ? a.pair_tok[p] : p;
+    }
+    __syncthreads();
+
+    const int row = blockIdx.y * kTileRows + wave * 16 + (lane & 15);
+    const int g = lane >> 4;
+    const int nblk = a.K / kBlk;
+    const uint8_t* WA = a.wa + (int64_t)e * a.w_exp_stride + (int64_t)row * (a.K / 2);
+    const uint8_t* SA = a.sa + (int64_t)e * a.s_exp_stride + (int64_t)row * nblk;
+    const uint8_t* WB = TWO ? a.wb + (int64_t)e * a.w_exp_stride + (int64_t)row * (a.K / 2) : nullptr;
+    const uint8_t* SB = TWO ? a.sb + (int64_t)e * a.s_exp_stride + (int64_t)row * nblk : nullptr;
+    // Activation tile loader: thread t copies 64 bytes (32 bf16) of token t/4,
+    // quarter t%4 of the super-step's 128 columns.
+    const int xr = t >> 2;
+    const int xq = t & 3;
+    const uint16_t* xsrc = a.act + (int64_t)s_row[xr] * a.act_stride + xq * 32;
+
+    const int S = a.K / kStep;
+    u32x4 wa_n = ld16_stream(WA + (int64_t)g * 16);
+    uint32_t sa_n = SA[g];
+    u32x4 wb_n{};
+    uint32_t sb_n = 0;
+    if constexpr (TWO) {
+        wb_n = ld16_stream(WB + (int64_t)g * 16);
+        sb_n = SB[g];
+    }
+    u32x4 xv_n[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xv_n[q] = reinterpret_cast<const u32x4*>(xsrc)[q];
+
+    f32x4 acc_a[4], acc_b[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        acc_a[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc_b[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s = 0; s < S; ++s) {
+        const u32x4 wa_c = wa_n;
+        const uint32_t sa_c = sa_n;
+        const u32x4 wb_c = wb_n;
+        const uint32_t sb_c = sb_n;
+        uint16_t* xb = xs[s & 1];
+        u32x4* xdst = reinterpret_cast<u32x4*>(xb + xr * kLdsRow + xq * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xdst[q] = xv_n[q];
+        if (s + 1 < S) {
+            const int blk = 4 * (s + 1) + g;
+            wa_n = ld16_stream(WA + (int64_t)blk * 16);
+            sa_n = SA[blk];
+            if constexpr (TWO) {
+                wb_n = ld16_stream(WB + (int64_t)blk * 16);
+                sb_n = SB[blk];
+            }
+            const u32x4* src = reinterpret_cast<const u32x4*>(xsrc + (s + 1) * kStep);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xv_n[q] = src[q];
+        }
+        __syncthreads();
+        bf16x8 opa[4], opb[4];
+        dequant_block(wa_c, sa_c, opa);
+        if constexpr (TWO) dequant_block(wb_c, sb_c, opb);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            if (b < nblk_tok) {
+                const uint16_t* xrow = xb + (16 * b + (lane & 15)) * kLdsRow + 32 * g;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bf16x8 xop = *reinterpret_cast<const bf16x8*>(xrow + 8 * j);
+                    acc_a[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(opa[j], xop, acc_a[b], 0, 0, 0);
+                    if constexpr (TWO)
+                        acc_b[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(opb[j], xop, acc_b[b], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // Epilogue: lane holds rows 4g..4g+3 of the wave's 16 (consecutive output
+    // columns of one pair row) for token column lane%16 of each block.
+    const int c0 = blockIdx.y * kTileRows + wave * 16 + 4 * g;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int j = 16 * b + (lane & 15);
+        if (b < nblk_tok && j < n) {
+            const int p = p0 + j;
+            if constexpr (TWO) {
+                uint32_t lo = f32_to_bf16_bits(silu_f32(acc_a[b][0]) * acc_b[b][0]) |
+                              ((uint32_t)f32_to_bf16_bits(silu_f32(acc_a[b][1]) * acc_b[b][1]) << 16);
+                uint32_t hi = f32_to_bf16_bits(silu_f32(acc_a[b][2]) * acc_b[b][2]) |
+                              ((uint32_t)f32_to_bf16_bits(silu_f32(acc_a[b][3]) * acc_b[b][3]) << 16);
+                *reinterpret_cast<uint2*>(a.M + (int64_t)p * a.rows + c0) = make_uint2(lo, hi);
+            } else {
+                const float wt = a.pair_w[p];
+                *reinterpret_cast<float4*>(a.Y + (int64_t)p * a.rows + c0) =
+                    make_float4(wt * acc_a[b][0], wt * acc_a[b][1], wt * acc_a[b][2], wt * acc_a[b][3]);
+            }
+        }
+    }
+}
+
+// out[t, o] = bf16( sum_k Y[pos(t, k), o] ), k in order; grid = (T, O / 1024).
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const float* Y, const int32_t* pos,
+                                                              int topk, int O, uint16_t* out) {
+    const int tok = blockIdx.x;
+    const int o = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if (o >= O) return;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < topk; ++k) {
+        const int p = pos[tok * topk + k];
+        if (p >= 0) {
+            const float4 v = *reinterpret_cast<const float4*>(Y + (int64_t)p * O + o);
+            s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+        }
+    }
+    const uint32_t lo = f32_to_bf16_bits(s.x) | ((uint32_t)f32_to_bf16_bits(s.y) << 16);
+    const uint32_t hi = f32_to_bf16_bits(s.z) | ((uint32_t)f32_to_bf16_bits(s.w) << 16);
+    *reinterpret_cast<uint2*>(out + (int64_t)tok * O + o) = make_uint2(lo, hi);
+}
+
+// ---------------------------------------------------------------- host ----
+
+uintptr_t align_up(uintptr_t v, uintptr_t a) { return (v + a - 1) / a * a; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct PrefillLayout {
+    size_t header, pair_tok, pair_w, pos, tile_e, tile_p0, tile_n, M, Y, total;
+    int max_tiles;
+};
+
+PrefillLayout prefill_layout(int T, int topk, int n_experts, int hidden, int out_dim) {
+    const size_t P = (size_t)T * topk;
+    PrefillLayout L;
+    L.max_tiles = (int)((P + kTileTok - 1) / kTileTok) + (n_experts < (int)P ? n_experts : (int)P);
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
+    L.header = take(16);
+    L.pair_tok = take(4 * P);
+    L.pair_w = take(4 * P);
+    L.pos = take(4 * P);
+    L.tile_e = take(4 * (size_t)L.max_tiles);
+    L.tile_p0 = take(4 * (size_t)L.max_tiles);
+    L.tile_n = take(4 * (size_t)L.max_tiles);
+    L.M = take(2 * P * (size_t)hidden);
+    L.Y = take(4 * P * (size_t)out_dim);
+    L.total = o + 256;
+    return L;
+}
+
+int prefill_validate(int T, int topk, int n_experts, int K_in, int hidden, int out_dim) {
+    if (K_in % kStep != 0 || K_in < kStep || K_in > kMaxRed) {
+        std::fprintf(stderr, "mxfp4_moe_prefill: K_in=%d must be a multiple of %d in [%d, %d]\n",
+                     K_in, kStep, kStep, kMaxRed);
+        return -1;
+    }
+    if (hidden % kStep != 0 || hidden < kStep || hidden > kMaxRed) {
+        std::fprintf(stderr, "mxfp4_moe_prefill: hidden=%d must be a multiple of %d in [%d, %d]\n",
+                     hidden, kStep, kStep, kMaxRed);
+        return -2;
+    }
+    if (out_dim % kTileRows != 0 || out_dim < kTileRows) {
+        std::fprintf(stderr, "mxfp4_moe_prefill: out_dim=%d not a positive multiple of %d\n",
+                     out_dim, kTileRows);
+        return -3;
+    }
+    if (T < 1 || T > kMaxTokens || topk < 1 || topk > kMaxTopk || n_experts < 1 ||
+        n_experts > kMaxExperts) {
+        std::fprintf(stderr, "mxfp4_moe_prefill: bad T=%d topk=%d n_experts=%d\n", T, topk,
+                     n_experts);
+        return -4;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" size_t mxfp4_moe_prefill_workspace_bytes(int T, int topk, int n_experts, int hidden,
+                                                    int out_dim) {
+    if (prefill_validate(T, topk, n_experts, kStep, hidden < kStep ? kStep : hidden,
+                         out_dim < kTileRows ? kTileRows : out_dim) != 0)
+        return 0;
+    return prefill_layout(T, topk, n_experts, hidden, out_dim).total;
+}
+
+extern "C" int mxfp4_moe_prefill(const dsv4_bf16_t* x, const uint8_t* W1_packed,
+                                 const uint8_t* W3_packed, const uint8_t* W2_packed,
+                                 const uint8_t* W1_scale, const uint8_t* W3_scale,
+                                 const uint8_t* W2_scale, const int32_t* ids, const float* weights,
+                                 int T, int topk, int n_experts, int K_in, int hidden, int out_dim,
+                                 dsv4_bf16_t* out, void* workspace, hipStream_t stream) {
+    int v = prefill_validate(T, topk, n_experts, K_in, hidden, out_dim);
+    if (v != 0) return v;
+    if (!x || !W1_packed || !W3_packed || !W2_packed || !W1_scale || !W3_scale || !W2_scale || !ids ||
+        !weights || !out || !workspace) {
+        std::fprintf(stderr, "mxfp4_moe_prefill: null operand\n");
+        return -3;
+    }
+    if (!aligned16(x) || !aligned16(W1_packed) || !aligned16(W3_packed) || !aligned16(W2_packed) ||
+        !aligned16(out)) {
+        std::fprintf(stderr, "mxfp4_moe_prefill: x, weights and out must be 16-byte aligned\n");
+        return -3;
+    }
+    const PrefillLayout L = prefill_layout(T, topk, n_experts, hidden, out_dim);
+    uint8_t* base = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(workspace), 256));
+    PrefillTables pt;
+    pt.header = reinterpret_cast<int32_t*>(base + L.header);
+    pt.pair_tok = reinterpret_cast<int32_t*>(base + L.pair_tok);
+    pt.pair_w = reinterpret_cast<float*>(base + L.pair_w);
+    pt.pos = reinterpret_cast<int32_t*>(base + L.pos);
+    pt.tile_e = reinterpret_cast<int32_t*>(base + L.tile_e);
+    pt.tile_p0 = reinterpret_cast<int32_t*>(base + L.tile_p0);
+    pt.tile_n = reinterpret_cast<int32_t*>(base + L.tile_n);
+    uint16_t* M = reinterpret_cast<uint16_t*>(base + L.M);
+    float* Y = reinterpret_cast<float*>(base + L.Y);
+    const int P = T * topk;
+
+    hipLaunchKernelGGL(prefill_route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, ids, weights,
+                       P, topk, n_experts, pt);
+    if (hipGetLastError() != hipSuccess) return -5;
+
+    GemmArgs A{};
+    A.act = reinterpret_cast<const uint16_t*>(x);
+    A.act_stride = K_in;
+    A.act_by_token = 1;
+    A.wa = W1_packed;
+    A.sa = W1_scale;
+    A.wb = W3_packed;
+    A.sb = W3_scale;
+    A.w_exp_stride = (int64_t)hidden * (K_in / 2);
+    A.s_exp_stride = (int64_t)hidden * (K_in / kBlk);
+    A.K = K_in;
+    A.rows = hidden;
+    A.header = pt.header;
+    A.tile_e = pt.tile_e;
+    A.tile_p0 = pt.tile_p0;
+    A.tile_n = pt.tile_n;
+    A.pair_tok = pt.pair_tok;
+    A.pair_w = pt.pair_w;
+    A.M = M;
+    hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3((unsigned)L.max_tiles, (unsigned)(hidden / kTileRows)),
+                       dim3(256), 0, stream, A);
+    if (hipGetLastError() != hipSuccess) return -6;
+
+    GemmArgs B = A;
+    B.act = M;
+    B.act_stride = hidden;
+    B.act_by_token = 0;
+    B.wa = W2_packed;
+    B.sa = W2_scale;
+    B.wb = nullptr;
+    B.sb = nullptr;
+    B.w_exp_stride = (int64_t)out_dim * (hidden / 2);
+    B.s_exp_stride = (int64_t)out_dim * (hidden / kBlk);
+    B.K = hidden;
+    B.rows = out_dim;
+    B.M = nullptr;
+    B.Y = Y;
+    hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)L.max_tiles, (unsigned)(out_dim / kTileRows)),
+                       dim3(256), 0, stream, B);
+    if (hipGetLastError() != hipSuccess) return -7;
+
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)T, (unsigned)((out_dim / 4 + 255) / 256)),
+                       dim3(256), 0, stream, Y, pt.pos, topk, out_dim, reinterpret_cast<uint16_t*>(out));
+    if (hipGetLastError() != hipSuccess) return -8;
+    return 0;
+}

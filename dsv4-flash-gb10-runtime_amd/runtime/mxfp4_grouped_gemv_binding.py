@@ -63,6 +63,10 @@ def _load_lib() -> ctypes.CDLL:
     lib.mxfp4_moe_down.argtypes = [_c_void_p] * 2 + [_c_int] * 5 + [_c_void_p] * 3
     lib.mxfp4_moe_layer.restype = _c_int
     lib.mxfp4_moe_layer.argtypes = [_c_void_p] * 8 + [_c_int] * 6 + [_c_void_p] * 5
+    lib.mxfp4_moe_prefill_workspace_bytes.restype = _c_size_t
+    lib.mxfp4_moe_prefill_workspace_bytes.argtypes = [_c_int] * 5
+    lib.mxfp4_moe_prefill.restype = _c_int
+    lib.mxfp4_moe_prefill.argtypes = [_c_void_p] * 9 + [_c_int] * 6 + [_c_void_p] * 3
     _LIB = lib
     return lib
 
@@ -223,6 +227,58 @@ def mxfp4_moe_grouped_gemv(
         _lib.vp(out), _lib.vp(workspace), ctypes.c_void_p(_lib.stream_ptr(x.device)))
     if rc != 0:
         raise RuntimeError(f"mxfp4_moe_grouped_gemv returned {rc}")
+    return out
+
+
+def prefill_workspace_bytes(T: int, topk: int, n_experts: int, hidden: int, out_dim: int) -> int:
+    return int(_load_lib().mxfp4_moe_prefill_workspace_bytes(T, topk, n_experts, hidden, out_dim))
+
+
+def mxfp4_moe_prefill(
+    x: torch.Tensor,
+    W1: Dict[str, torch.Tensor],
+    W3: Dict[str, torch.Tensor],
+    W2: Dict[str, torch.Tensor],
+    ids: torch.Tensor,
+    weights: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Routed SwiGLU for a prefill chunk of T tokens on the matrix cores
+    (same result as mxfp4_moe_grouped_gemv); returns bf16 [T, out_dim]."""
+    lib = _load_lib()
+    _check(x, "x", torch.bfloat16)
+    _check(ids, "ids", torch.int32)
+    _check(weights, "weights", torch.float32)
+    _check_mats(W1, W3, W2)
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    T, K_in = x.shape
+    n_experts, hidden, out_dim = _shapes(W1, W3, W2, K_in)
+    if ids.dim() != 2 or ids.shape[0] != T or tuple(weights.shape) != tuple(ids.shape):
+        raise ValueError(f"ids/weights must both be [T={T}, topk]")
+    topk = ids.shape[1]
+    if out is None:
+        out = torch.empty(T, out_dim, dtype=torch.bfloat16, device=x.device)
+    else:
+        _check(out, "out", torch.bfloat16)
+        if out.numel() != T * out_dim:
+            raise ValueError(f"out numel {out.numel()} != {T * out_dim}")
+    ws_bytes = prefill_workspace_bytes(T, topk, n_experts, hidden, out_dim)
+    if ws_bytes == 0:
+        raise ValueError(f"unsupported prefill shape T={T} topk={topk} E={n_experts} "
+                         f"K={K_in} H={hidden} O={out_dim}")
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() * workspace.element_size() < ws_bytes:
+        raise ValueError(f"workspace smaller than {ws_bytes} bytes")
+    rc = lib.mxfp4_moe_prefill(
+        _lib.vp(x), _lib.vp(W1["packed"]), _lib.vp(W3["packed"]), _lib.vp(W2["packed"]),
+        _lib.vp(W1["scale"]), _lib.vp(W3["scale"]), _lib.vp(W2["scale"]),
+        _lib.vp(ids), _lib.vp(weights), T, topk, n_experts, K_in, hidden, out_dim,
+        _lib.vp(out), _lib.vp(workspace), ctypes.c_void_p(_lib.stream_ptr(x.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_prefill returned {rc}")
     return out
 
 

@@ -135,6 +135,27 @@ int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
                     dsv4_bf16_t* out, int32_t* ids_out, float* weights_out, void* workspace,
                     hipStream_t stream);
 
+/* EXTENSION (no reference counterpart; the reference has no prefill MoE path,
+ * SURVEY mismatch M6): the routed MoE layer for a chunk of many tokens on the
+ * matrix cores. Same result as mxfp4_moe_grouped_gemv for every token:
+ *   out[t] = bf16( sum_k weights[t,k] * W2_e . bf16(silu(W1_e x_t) * (W3_e x_t)) ), e = ids[t,k]
+ * with the MXFP4 weights dequantised exactly to bf16 and multiplied on
+ * v_mfma_f32_16x16x32_bf16 (fp32 accumulate). x [T, K_in] bf16 (16-byte
+ * aligned), ids/weights [T, topk], out [T, out_dim] bf16. Ids outside
+ * [0, n_experts) contribute nothing. Four launches, no allocation; workspace
+ * of mxfp4_moe_prefill_workspace_bytes bytes (0 for invalid arguments).
+ * Returns 0; -1 K_in not a multiple of 128 in [128, 8192]; -2 hidden likewise;
+ * -3 out_dim not a positive multiple of 64, a null or unaligned operand; -4 T outside
+ * [1, 16384], topk outside [1, 16] or n_experts outside [1, 1024]; -5..-8
+ * launch failure of routing / stage A / stage B / combine. */
+size_t mxfp4_moe_prefill_workspace_bytes(int T, int topk, int n_experts, int hidden, int out_dim);
+int mxfp4_moe_prefill(const dsv4_bf16_t* x,
+                      const uint8_t* W1_packed, const uint8_t* W3_packed, const uint8_t* W2_packed,
+                      const uint8_t* W1_scale, const uint8_t* W3_scale, const uint8_t* W2_scale,
+                      const int32_t* ids, const float* weights, int T, int topk, int n_experts,
+                      int K_in, int hidden, int out_dim, dsv4_bf16_t* out, void* workspace,
+                      hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* libmxfp4_gemv.so                                                          */
 /* ------------------------------------------------------------------------ */

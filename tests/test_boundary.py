@@ -19,7 +19,8 @@ LIBS = {
     "mxfp4-routed/libmxfp4_grouped_gemv.so": [
         "mxfp4_grouped_gemv_topk", "mxfp4_grouped_workspace_bytes",
         "mxfp4_moe_route_sigmoid_topk", "mxfp4_moe_workspace_bytes", "mxfp4_moe_grouped_gemv",
-        "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer"],
+        "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer",
+        "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_dequant_bf16"],
     "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],
@@ -122,6 +123,33 @@ def test_moe_validation_codes():
     wb.argtypes = [ctypes.c_int] * 4
     assert wb(16, 8, 256, 2048) >= 16 * 8 * 2048 * 2
     assert wb(0, 8, 256, 2048) == 0
+
+
+def test_prefill_validation_codes():
+    lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
+    P = ctypes.c_void_p
+    fn = lib.mxfp4_moe_prefill
+    fn.restype = ctypes.c_int
+    fn.argtypes = [P] * 9 + [ctypes.c_int] * 6 + [P] * 3
+    ws = lib.mxfp4_moe_prefill_workspace_bytes
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [ctypes.c_int] * 5
+
+    def call(T, topk, E, K, H, O):
+        return fn(*([None] * 9), T, topk, E, K, H, O, None, None, None)
+
+    assert call(512, 8, 256, 4000, 2048, 4096) == -1      # K_in % 128
+    assert call(512, 8, 256, 16384, 2048, 4096) == -1     # K_in > 8192
+    assert call(512, 8, 256, 4096, 2000, 4096) == -2      # hidden % 128
+    assert call(512, 8, 256, 4096, 2048, 4000) == -3      # out_dim % 64
+    assert call(0, 8, 256, 4096, 2048, 4096) == -4        # T < 1
+    assert call(512, 17, 256, 4096, 2048, 4096) == -4     # topk > 16
+    assert call(512, 8, 2048, 4096, 2048, 4096) == -4     # n_experts > 1024
+    assert call(512, 8, 256, 4096, 2048, 4096) == -3      # null operands
+    assert ws(0, 8, 256, 2048, 4096) == 0
+    big = ws(512, 8, 256, 2048, 4096)
+    # M [P, H] bf16 + Y [P, O] fp32 dominate
+    assert big >= 4096 * 2048 * 2 + 4096 * 4096 * 4
 
 
 def test_dense_validation_codes():
