@@ -177,27 +177,21 @@ __device__ __forceinline__ void dequant_block(u32x4 w, uint32_t s, bf16x8* op) {
     }
 }
 
-// grid = (max_tiles, rows / 64), block = 256. TWO: stage A (W1 and W3, SwiGLU
-// epilogue into M); otherwise stage B (W2, weighted fp32 rows into Y).
-template <bool TWO>
-__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) {
-    __shared__ __align__(16) uint16_t xs[2][kTileTok * kLdsRow];   // 2 x 17 KB
-    __shared__ int s_row[kTileTok];
-    const int ti = blockIdx.x;
-    if (ti >= a.header[0]) return;                                  // whole workgroup
+// The GEMM of one tile with NTB (1..4) blocks of 16 tokens. The weights and
+// the activation pieces of the next kDepth super-steps are kept in flight in
+// registers (loads clamped to the last super-step, never conditional); each
+// super-step's activation tile is written to one of two LDS buffers before
+// the barrier that precedes its multiply.
+// K is a multiple of kDepth * 128, so the unrolled loop has no branches.
+constexpr int kDepth = 4;
+
+template <bool TWO, int NTB, int SFIX>
+__device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int p0, int n,
+                                                  uint16_t (*xs)[kTileTok * kLdsRow],
+                                                  const int* s_row) {
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int e = a.tile_e[ti];
-    const int p0 = a.tile_p0[ti];
-    const int n = a.tile_n[ti];
-    const int nblk_tok = (n + 15) / 16;
-    if (t < kTileTok) {
-        const int p = p0 + min(t, n - 1);
-        s_row[t] = a.act_by_token ? a.pair_tok[p] : p;
-    }
-    __syncthreads();
-
     const int row = blockIdx.y * kTileRows + wave * 16 + (lane & 15);
     const int g = lane >> 4;
     const int nblk = a.K / kBlk;
@@ -205,59 +199,75 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) 
     const uint8_t* SA = a.sa + (int64_t)e * a.s_exp_stride + (int64_t)row * nblk;
     const uint8_t* WB = TWO ? a.wb + (int64_t)e * a.w_exp_stride + (int64_t)row * (a.K / 2) : nullptr;
     const uint8_t* SB = TWO ? a.sb + (int64_t)e * a.s_exp_stride + (int64_t)row * nblk : nullptr;
-    // Activation tile loader: thread t copies 64 bytes (32 bf16) of token t/4,
-    // quarter t%4 of the super-step's 128 columns.
-    const int xr = t >> 2;
-    const int xq = t & 3;
-    const uint16_t* xsrc = a.act + (int64_t)s_row[xr] * a.act_stride + xq * 32;
+    // SFIX > 0: the super-step count is a compile-time constant and the loop
+    // is unrolled completely, which keeps every wait for an in-flight load
+    // exact (a wait at the top of a rolled loop covers all loads in flight).
+    const int S = SFIX > 0 ? SFIX : a.K / kStep;
 
-    const int S = a.K / kStep;
-    u32x4 wa_n = ld16_stream(WA + (int64_t)g * 16);
-    uint32_t sa_n = SA[g];
-    u32x4 wb_n{};
-    uint32_t sb_n = 0;
-    if constexpr (TWO) {
-        wb_n = ld16_stream(WB + (int64_t)g * 16);
-        sb_n = SB[g];
+    // Activation tile: 16*NTB token rows x 128 columns, 16 bytes per thread
+    // per token block: piece t + 256*i is row (t + 256*i) / 16, columns
+    // 8*((t + 256*i) % 16) .. +8.
+    const uint16_t* xsrc[NTB];
+    int xoff[NTB];
+#pragma unroll
+    for (int i = 0; i < NTB; ++i) {
+        const int pi = t + 256 * i;
+        xsrc[i] = a.act + (int64_t)s_row[pi >> 4] * a.act_stride + (pi & 15) * 8;
+        xoff[i] = (pi >> 4) * kLdsRow + (pi & 15) * 8;
     }
-    u32x4 xv_n[4];
+    u32x4 xv[kDepth][NTB];
+    auto load_x = [&](int d, int s) {
+        const int so = min(s, S - 1) * kStep;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xv_n[q] = reinterpret_cast<const u32x4*>(xsrc)[q];
+        for (int i = 0; i < NTB; ++i) xv[d][i] = *reinterpret_cast<const u32x4*>(xsrc[i] + so);
+    };
+    u32x4 wa_r[kDepth], wb_r[kDepth];
+    uint32_t sa_r[kDepth], sb_r[kDepth];
+    auto load_w = [&](int d, int s) {
+        const int blk = 4 * min(s, S - 1) + g;
+        wa_r[d] = ld16_stream(WA + (int64_t)blk * 16);
+        sa_r[d] = SA[blk];
+        if constexpr (TWO) {
+            wb_r[d] = ld16_stream(WB + (int64_t)blk * 16);
+            sb_r[d] = SB[blk];
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        load_x(d, d);
+        load_w(d, d);
+    }
 
-    f32x4 acc_a[4], acc_b[4];
+    f32x4 acc_a[NTB], acc_b[NTB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < NTB; ++b) {
         acc_a[b] = f32x4{0.f, 0.f, 0.f, 0.f};
         acc_b[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int s = 0; s < S; ++s) {
-        const u32x4 wa_c = wa_n;
-        const uint32_t sa_c = sa_n;
-        const u32x4 wb_c = wb_n;
-        const uint32_t sb_c = sb_n;
-        uint16_t* xb = xs[s & 1];
-        u32x4* xdst = reinterpret_cast<u32x4*>(xb + xr * kLdsRow + xq * 32);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xdst[q] = xv_n[q];
-        if (s + 1 < S) {
-            const int blk = 4 * (s + 1) + g;
-            wa_n = ld16_stream(WA + (int64_t)blk * 16);
-            sa_n = SA[blk];
+    for (int s0 = 0; s0 < (SFIX > 0 ? SFIX : S); s0 += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            const int s = s0 + d;
+            uint16_t* xb = xs[d & 1];          // s & 1 (s0 is a multiple of kDepth)
+#pragma unroll
+            for (int i = 0; i < NTB; ++i) *reinterpret_cast<u32x4*>(xb + xoff[i]) = xv[d][i];
+            load_x(d, s + kDepth);
+            const u32x4 wa_c = wa_r[d];
+            const uint32_t sa_c = sa_r[d];
+            u32x4 wb_c{};
+            uint32_t sb_c = 0;
             if constexpr (TWO) {
-                wb_n = ld16_stream(WB + (int64_t)blk * 16);
-                sb_n = SB[blk];
+                wb_c = wb_r[d];
+                sb_c = sb_r[d];
             }
-            const u32x4* src = reinterpret_cast<const u32x4*>(xsrc + (s + 1) * kStep);
+            load_w(d, s + kDepth);
+            __syncthreads();
+            bf16x8 opa[4], opb[4];
+            dequant_block(wa_c, sa_c, opa);
+            if constexpr (TWO) dequant_block(wb_c, sb_c, opb);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) xv_n[q] = src[q];
-        }
-        __syncthreads();
-        bf16x8 opa[4], opb[4];
-        dequant_block(wa_c, sa_c, opa);
-        if constexpr (TWO) dequant_block(wb_c, sb_c, opb);
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            if (b < nblk_tok) {
+            for (int b = 0; b < NTB; ++b) {
                 const uint16_t* xrow = xb + (16 * b + (lane & 15)) * kLdsRow + 32 * g;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -273,15 +283,15 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) 
     // columns of one pair row) for token column lane%16 of each block.
     const int c0 = blockIdx.y * kTileRows + wave * 16 + 4 * g;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < NTB; ++b) {
         const int j = 16 * b + (lane & 15);
-        if (b < nblk_tok && j < n) {
+        if (j < n) {
             const int p = p0 + j;
             if constexpr (TWO) {
-                uint32_t lo = f32_to_bf16_bits(silu_f32(acc_a[b][0]) * acc_b[b][0]) |
-                              ((uint32_t)f32_to_bf16_bits(silu_f32(acc_a[b][1]) * acc_b[b][1]) << 16);
-                uint32_t hi = f32_to_bf16_bits(silu_f32(acc_a[b][2]) * acc_b[b][2]) |
-                              ((uint32_t)f32_to_bf16_bits(silu_f32(acc_a[b][3]) * acc_b[b][3]) << 16);
+                const uint32_t lo = f32_to_bf16_bits(silu_f32(acc_a[b][0]) * acc_b[b][0]) |
+                                    ((uint32_t)f32_to_bf16_bits(silu_f32(acc_a[b][1]) * acc_b[b][1]) << 16);
+                const uint32_t hi = f32_to_bf16_bits(silu_f32(acc_a[b][2]) * acc_b[b][2]) |
+                                    ((uint32_t)f32_to_bf16_bits(silu_f32(acc_a[b][3]) * acc_b[b][3]) << 16);
                 *reinterpret_cast<uint2*>(a.M + (int64_t)p * a.rows + c0) = make_uint2(lo, hi);
             } else {
                 const float wt = a.pair_w[p];
@@ -290,6 +300,39 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) 
             }
         }
     }
+}
+
+// grid = (max_tiles, rows / 64), block = 256. TWO: stage A (W1 and W3, SwiGLU
+// epilogue into M); otherwise stage B (W2, weighted fp32 rows into Y). The
+// tile's token-block count selects a specialised body.
+template <bool TWO>
+__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) {
+    __shared__ __align__(16) uint16_t xs[2][kTileTok * kLdsRow];   // 2 x 17 KB
+    __shared__ int s_row[kTileTok];
+    const int ti = blockIdx.x;
+    if (ti >= a.header[0]) return;                                  // whole workgroup
+    const int t = threadIdx.x;
+    const int e = a.tile_e[ti];
+    const int p0 = a.tile_p0[ti];
+    const int n = a.tile_n[ti];
+    if (t < kTileTok) {
+        const int p = p0 + min(t, n - 1);
+        s_row[t] = a.act_by_token ? a.pair_tok[p] : p;
+    }
+    __syncthreads();
+    const int S = a.K / kStep;
+#define DSV4_TILES(SV)                                                          \
+    switch ((n + 15) / 16) {                                                    \
+        case 1: prefill_gemm_tile<TWO, 1, SV>(a, e, p0, n, xs, s_row); break;  \
+        case 2: prefill_gemm_tile<TWO, 2, SV>(a, e, p0, n, xs, s_row); break;  \
+        case 3: prefill_gemm_tile<TWO, 3, SV>(a, e, p0, n, xs, s_row); break;  \
+        default: prefill_gemm_tile<TWO, 4, SV>(a, e, p0, n, xs, s_row); break; \
+    }
+    if (S == 32) { DSV4_TILES(32) }
+    else if (S == 16) { DSV4_TILES(16) }
+    else if (S == 4) { DSV4_TILES(4) }
+    else { DSV4_TILES(0) }
+#undef DSV4_TILES
 }
 
 // out[t, o] = bf16( sum_k Y[pos(t, k), o] ), k in order; grid = (T, O / 1024).
@@ -341,14 +384,15 @@ PrefillLayout prefill_layout(int T, int topk, int n_experts, int hidden, int out
 }
 
 int prefill_validate(int T, int topk, int n_experts, int K_in, int hidden, int out_dim) {
-    if (K_in % kStep != 0 || K_in < kStep || K_in > kMaxRed) {
+    constexpr int kRed = kStep * kDepth;   // whole groups of super-steps
+    if (K_in % kRed != 0 || K_in < kRed || K_in > kMaxRed) {
         std::fprintf(stderr, "mxfp4_moe_prefill: K_in=%d must be a multiple of %d in [%d, %d]\n",
-                     K_in, kStep, kStep, kMaxRed);
+                     K_in, kRed, kRed, kMaxRed);
         return -1;
     }
-    if (hidden % kStep != 0 || hidden < kStep || hidden > kMaxRed) {
+    if (hidden % kRed != 0 || hidden < kRed || hidden > kMaxRed) {
         std::fprintf(stderr, "mxfp4_moe_prefill: hidden=%d must be a multiple of %d in [%d, %d]\n",
-                     hidden, kStep, kStep, kMaxRed);
+                     hidden, kRed, kRed, kMaxRed);
         return -2;
     }
     if (out_dim % kTileRows != 0 || out_dim < kTileRows) {
@@ -369,7 +413,7 @@ int prefill_validate(int T, int topk, int n_experts, int K_in, int hidden, int o
 
 extern "C" size_t mxfp4_moe_prefill_workspace_bytes(int T, int topk, int n_experts, int hidden,
                                                     int out_dim) {
-    if (prefill_validate(T, topk, n_experts, kStep, hidden < kStep ? kStep : hidden,
+    if (prefill_validate(T, topk, n_experts, kStep * kDepth, hidden,
                          out_dim < kTileRows ? kTileRows : out_dim) != 0)
         return 0;
     return prefill_layout(T, topk, n_experts, hidden, out_dim).total;

@@ -144,7 +144,7 @@ int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
  * aligned), ids/weights [T, topk], out [T, out_dim] bf16. Ids outside
  * [0, n_experts) contribute nothing. Four launches, no allocation; workspace
  * of mxfp4_moe_prefill_workspace_bytes bytes (0 for invalid arguments).
- * Returns 0; -1 K_in not a multiple of 128 in [128, 8192]; -2 hidden likewise;
+ * Returns 0; -1 K_in not a multiple of 512 in [512, 8192]; -2 hidden likewise;
  * -3 out_dim not a positive multiple of 64, a null or unaligned operand; -4 T outside
  * [1, 16384], topk outside [1, 16] or n_experts outside [1, 1024]; -5..-8
  * launch failure of routing / stage A / stage B / combine. */

@@ -329,7 +329,7 @@ def test_moe_indexed_equals_packed_dropin(device):
 def test_moe_prefill_small_vs_oracle(device, T, topk, E):
     """MFMA prefill path against the oracle at small dims, including a
     duplicate id in a token and ids outside [0, n_experts)."""
-    K, H, O = 512, 256, 384
+    K, H, O = 512, 512, 384
     announce(f"mxfp4_moe_prefill T={T} topk={topk} E={E} K={K} H={H} O={O}")
     W1p, W1s = synth.mxfp4_weight(8400 + E, H, K, E)
     W3p, W3s = synth.mxfp4_weight(8404 + E, H, K, E)
