@@ -252,6 +252,21 @@ __device__ __forceinline__ int wave_min_i32(int v) {
     });
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    return wave_allreduce_u32(v, [](uint32_t a, uint32_t b) { return max(a, b); });
+}
+
+// Order-preserving key of a non-NaN float: a > b exactly when key(a) >
+// key(b), except that -0 and +0 get different keys (callers map -0 to +0).
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
 __device__ __forceinline__ float wave_sum_f32(float v) {
     return __uint_as_float(wave_allreduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
         return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));

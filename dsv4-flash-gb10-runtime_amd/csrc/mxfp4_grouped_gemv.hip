@@ -198,44 +198,54 @@ __device__ __forceinline__ float scale_of(uint32_t packed, int j) {
 
 // Top-k of one token's logits on one wave: descending, ties to the lower
 // expert index, weights sigmoid(l) renormalised to sum 1. Lane k < topk
-// returns the k-th pick. Each lane holds PER logits (expert lane + 64*i);
-// each round takes the wave maximum (DPP), then the lowest index holding it;
-// a picked entry becomes NaN, which fmaxf and the comparisons ignore. NaN
-// logits rank as -inf.
+// returns the k-th pick. Each lane holds PER logits (expert lane + 64*i) as
+// order-preserving integer keys (larger logit <-> larger key; -0 is taken as
+// +0 and NaN as -inf, so equal logits give equal keys); entries past
+// n_experts and picked entries are key 0, below every logit. Each round is
+// one integer max reduction; the winner's index comes from one ballot per
+// element slot (lowest slot first, then lowest lane: the lowest expert
+// index among equal keys) and is removed by a select.
 template <int PER>
 __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk,
                                                   int lane, int& my_e, float& my_w) {
-    const float kRemoved = __uint_as_float(0x7FC00000u);
-    float v[PER];
-    // Unconditional loads (index clamped into the row) so all of them are in
-    // flight together; entries past n_experts become "removed".
+    // Unconditional loads (index clamped into the row), all in flight
+    // together: the empty asm keeps the compiler from moving a load into the
+    // e < n_experts branch, where each would wait for the one before.
+    float lv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) lv[i] = lt[min(lane + 64 * i, n_experts - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(lv[i]));
+    uint32_t kv[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        float l = lt[min(e, n_experts - 1)];
-        l = (l != l) ? -INFINITY : l;
-        v[i] = e < n_experts ? l : kRemoved;
+        const float l = (lv[i] != lv[i]) ? -INFINITY : (lv[i] == 0.f ? 0.f : lv[i]);
+        kv[i] = lane + 64 * i < n_experts ? order_key(l) : 0u;
     }
-    my_e = 0;
-    float my_l = -INFINITY;
+    int me = 0;
+    uint32_t mk = 0;
     for (int k = 0; k < topk; ++k) {
-        float best = v[0];
+        uint32_t best = kv[0];
 #pragma unroll
-        for (int i = 1; i < PER; ++i) best = fmaxf(best, v[i]);
-        const float wmax = wave_max_f32(best);
-        int idx = 0x7FFFFFFF;
+        for (int i = 1; i < PER; ++i) best = max(best, kv[i]);
+        const uint32_t m = __builtin_amdgcn_readfirstlane(wave_max_u32(best));
+        // The last (lowest) slot whose ballot is not empty holds the pick.
+        int idx = 0;
 #pragma unroll
-        for (int i = PER - 1; i >= 0; --i)
-            if (v[i] == wmax) idx = lane + 64 * i;
-        idx = wave_min_i32(idx);
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (lane + 64 * i == idx) v[i] = kRemoved;
-        if (lane == k) {
-            my_e = idx;
-            my_l = wmax;
+        for (int i = PER - 1; i >= 0; --i) {
+            const uint64_t b = __ballot(kv[i] == m);
+            if (b != 0) idx = 64 * i + __builtin_ctzll(b);
         }
+        const bool hit = lane == (idx & 63);
+        const int slot = idx >> 6;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) kv[i] = (hit && slot == i) ? 0u : kv[i];
+        me = lane == k ? idx : me;
+        mk = lane == k ? m : mk;
     }
+    my_e = me;
+    const float my_l = lane < topk ? key_value(mk) : -INFINITY;
     const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
     my_w = s / wave_sum_f32(s);
 }

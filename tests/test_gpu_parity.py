@@ -217,6 +217,44 @@ def test_route_sigmoid_topk(device):
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6)
 
 
+def _gating_edge_logits():
+    """Logit sets with equal values, signed zeros, -inf, NaN and expert counts
+    that are not multiples of 64 (the wave holds 4, 8 or 16 logits per lane)."""
+    rng = np.random.default_rng(7100)
+    cases = []
+    cases.append(("halves", np.round(rng.standard_normal((4, 256)) * 2) / 2, 8))
+    z = np.zeros((2, 256), dtype=np.float32)
+    z[:, ::3] = -0.0
+    z[0, [7, 90, 200]] = [1.0, 2.0, 1.0]
+    z[1, 250] = -1.0
+    cases.append(("signed zeros", z, 8))
+    ni = np.full((2, 256), -np.inf, dtype=np.float32)
+    ni[0, [3, 77, 130]] = [0.5, -2.0, 0.5]
+    cases.append(("minus inf", ni, 8))
+    na = rng.standard_normal((2, 256)).astype(np.float32)
+    na[:, 1::4] = np.nan
+    cases.append(("nan entries", na, 8))
+    cases.append(("E=200 k=16", rng.standard_normal((3, 200)), 16))
+    cases.append(("E=300 k=5", rng.standard_normal((3, 300)), 5))
+    cases.append(("E=1024 k=8", np.round(rng.standard_normal((2, 1024)) * 4) / 4, 8))
+    cases.append(("E=8 k=8", rng.standard_normal((2, 8)), 8))
+    return cases
+
+
+@pytest.mark.parametrize("name,logits,k", _gating_edge_logits(), ids=lambda v: v if isinstance(v, str) else "")
+def test_route_sigmoid_topk_edges(device, name, logits, k):
+    """Ties go to the lower expert index, -0 equals +0, NaN ranks as -inf (the
+    NaN case keeps enough finite logits that no NaN is picked, where the
+    oracle's ordering of NaN below -inf would differ)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    announce(f"mxfp4_moe_route_sigmoid_topk edge case {name} E={logits.shape[1]} k={k}")
+    ids, w = gb.route_sigmoid_topk(dev_f32(logits, device), k)
+    rids, rw = mx.route_sigmoid_topk(logits, k)
+    assert np.array_equal(ids.cpu().numpy(), rids), name
+    # a token whose logits are all -inf gets 0/0 weights in both
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6, equal_nan=True), name
+
+
 @pytest.mark.parametrize("T", [1, 4, 16])
 def test_moe_indexed_small_dims(device, T):
     """All T of the config at reduced K/H/O so the oracle covers every expert quickly."""
