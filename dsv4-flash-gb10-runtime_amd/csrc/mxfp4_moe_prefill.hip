@@ -177,32 +177,59 @@ __device__ __forceinline__ void dequant_block(u32x4 w, uint32_t s, bf16x8* op) {
     }
 }
 
-// The GEMM of one tile with NTB (1..4) blocks of 16 tokens. The weights and
-// the activation pieces of the next kDepth super-steps are kept in flight in
-// registers (loads clamped to the last super-step, never conditional); each
-// super-step's activation tile is written to one of two LDS buffers before
-// the barrier that precedes its multiply.
-// K is a multiple of kDepth * 128, so the unrolled loop has no branches.
-constexpr int kDepth = 4;
+// The GEMM of one tile with NTB (1..4) blocks of 16 tokens. The weights of
+// the next DW super-steps and the activation pieces of the next kDX are kept
+// in flight in registers: weights stream from HBM and need the deeper ring,
+// activations are re-read by every row block of the tile and mostly hit L2.
+// Each super-step's activation tile is written to one of two LDS buffers
+// before the barrier that precedes its multiply.
+// SFIX > 0: the super-step count is a compile-time constant and the loop is
+// unrolled completely; loads past the last super-step are then dropped at
+// compile time and every wait for an in-flight load is exact (a wait at the
+// top of a rolled loop covers all loads in flight). The rolled path (SFIX 0)
+// needs S to be a multiple of DW and clamps loads to the last super-step.
+constexpr int kDepth = 4;   // super-steps per group of the rolled path (K granule = 512)
+constexpr int kDX = 2;
+constexpr int kDWDeep = 8;  // weight ring of the unrolled common-K bodies
 
-template <bool TWO, int NTB, int SFIX>
-__device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int p0, int n,
+template <bool TWO, int NTB, int SFIX, int DW>
+__device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int p0, int n, int rb,
                                                   uint16_t (*xs)[kTileTok * kLdsRow],
-                                                  const int* s_row) {
+                                                  const int* s_row, uint8_t* sl) {
+    static_assert(DW % kDX == 0 && (SFIX == 0 || SFIX % DW == 0), "ring depths");
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int row = blockIdx.y * kTileRows + wave * 16 + (lane & 15);
+    const int rl = wave * 16 + (lane & 15);           // row within the 64-row block
+    const int row = rb * kTileRows + rl;
     const int g = lane >> 4;
     const int nblk = a.K / kBlk;
     const uint8_t* WA = a.wa + (int64_t)e * a.w_exp_stride + (int64_t)row * (a.K / 2);
-    const uint8_t* SA = a.sa + (int64_t)e * a.s_exp_stride + (int64_t)row * nblk;
     const uint8_t* WB = TWO ? a.wb + (int64_t)e * a.w_exp_stride + (int64_t)row * (a.K / 2) : nullptr;
-    const uint8_t* SB = TWO ? a.sb + (int64_t)e * a.s_exp_stride + (int64_t)row * nblk : nullptr;
-    // SFIX > 0: the super-step count is a compile-time constant and the loop
-    // is unrolled completely, which keeps every wait for an in-flight load
-    // exact (a wait at the top of a rolled loop covers all loads in flight).
     const int S = SFIX > 0 ? SFIX : a.K / kStep;
+
+    // Scale tile: the block's 64 scale rows of each matrix are one contiguous
+    // run of 64*nblk bytes; 16 bytes per thread per piece, staged in LDS
+    // (sl: matrix A, then matrix B) before the first barrier of the loop.
+    const int spieces = kTileRows * nblk / 16;          // per matrix: 256 .. 1024
+    const u32x4* SAt = reinterpret_cast<const u32x4*>(a.sa + (int64_t)e * a.s_exp_stride + (int64_t)rb * kTileRows * nblk);
+    const u32x4* SBt = TWO ? reinterpret_cast<const u32x4*>(a.sb + (int64_t)e * a.s_exp_stride + (int64_t)rb * kTileRows * nblk) : nullptr;
+    // pieces per thread: exact for a compile-time K, else at the K cap
+    constexpr int kSAll = (TWO ? 2 : 1) * kTileRows * (SFIX > 0 ? 4 * SFIX : kMaxRed / kBlk) / 16;
+    constexpr int kSPer = (kSAll + 255) / 256;
+    u32x4 sv[kSPer];
+#pragma unroll
+    for (int i = 0; i < kSPer; ++i) {
+        const int q = t + 256 * i;                          // piece index over A then B
+        const int qa = min(q, spieces - 1);
+        if constexpr (TWO) {
+            const int qb = min(max(q - spieces, 0), spieces - 1);
+            sv[i] = q < spieces ? SAt[qa] : SBt[qb];
+        } else {
+            sv[i] = SAt[qa];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     // Activation tile: 16*NTB token rows x 128 columns, 16 bytes per thread
     // per token block: piece t + 256*i is row (t + 256*i) / 16, columns
@@ -215,28 +242,33 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
         xsrc[i] = a.act + (int64_t)s_row[pi >> 4] * a.act_stride + (pi & 15) * 8;
         xoff[i] = (pi >> 4) * kLdsRow + (pi & 15) * 8;
     }
-    u32x4 xv[kDepth][NTB];
+    u32x4 xv[kDX][NTB];
     auto load_x = [&](int d, int s) {
+        if (SFIX > 0 && s >= S) return;              // compile-time in the unrolled body
         const int so = min(s, S - 1) * kStep;
 #pragma unroll
         for (int i = 0; i < NTB; ++i) xv[d][i] = *reinterpret_cast<const u32x4*>(xsrc[i] + so);
     };
-    u32x4 wa_r[kDepth], wb_r[kDepth];
-    uint32_t sa_r[kDepth], sb_r[kDepth];
+    u32x4 wa_r[DW], wb_r[DW];
     auto load_w = [&](int d, int s) {
+        if (SFIX > 0 && s >= S) return;
         const int blk = 4 * min(s, S - 1) + g;
         wa_r[d] = ld16_stream(WA + (int64_t)blk * 16);
-        sa_r[d] = SA[blk];
-        if constexpr (TWO) {
-            wb_r[d] = ld16_stream(WB + (int64_t)blk * 16);
-            sb_r[d] = SB[blk];
-        }
+        if constexpr (TWO) wb_r[d] = ld16_stream(WB + (int64_t)blk * 16);
     };
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        load_x(d, d);
-        load_w(d, d);
+    for (int d = 0; d < kDX; ++d) load_x(d, d);
+#pragma unroll
+    for (int d = 0; d < DW; ++d) load_w(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4* slv = reinterpret_cast<u32x4*>(sl);
+#pragma unroll
+    for (int i = 0; i < kSPer; ++i) {
+        const int q = t + 256 * i;
+        if (q < (TWO ? 2 : 1) * spieces) slv[q] = sv[i];
     }
+    const uint8_t* sla = sl + rl * nblk + g;               // + 4*s: this lane's block of super-step s
+    const uint8_t* slb = sl + spieces * 16 + rl * nblk + g;
 
     f32x4 acc_a[NTB], acc_b[NTB];
 #pragma unroll
@@ -245,24 +277,22 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
         acc_b[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int s0 = 0; s0 < (SFIX > 0 ? SFIX : S); s0 += kDepth) {
+    for (int s0 = 0; s0 < (SFIX > 0 ? SFIX : S); s0 += DW) {
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) {
+        for (int d = 0; d < DW; ++d) {
             const int s = s0 + d;
-            uint16_t* xb = xs[d & 1];          // s & 1 (s0 is a multiple of kDepth)
+            const int dx = d % kDX;
+            uint16_t* xb = xs[d & 1];          // s & 1 (s0 is a multiple of DW, DW even)
 #pragma unroll
-            for (int i = 0; i < NTB; ++i) *reinterpret_cast<u32x4*>(xb + xoff[i]) = xv[d][i];
-            load_x(d, s + kDepth);
+            for (int i = 0; i < NTB; ++i) *reinterpret_cast<u32x4*>(xb + xoff[i]) = xv[dx][i];
+            load_x(dx, s + kDX);
             const u32x4 wa_c = wa_r[d];
-            const uint32_t sa_c = sa_r[d];
             u32x4 wb_c{};
-            uint32_t sb_c = 0;
-            if constexpr (TWO) {
-                wb_c = wb_r[d];
-                sb_c = sb_r[d];
-            }
-            load_w(d, s + kDepth);
+            if constexpr (TWO) wb_c = wb_r[d];
+            load_w(d, s + DW);
             __syncthreads();
+            const uint32_t sa_c = sla[4 * s];
+            const uint32_t sb_c = TWO ? slb[4 * s] : 0u;
             bf16x8 opa[4], opb[4];
             dequant_block(wa_c, sa_c, opa);
             if constexpr (TWO) dequant_block(wb_c, sb_c, opb);
@@ -281,7 +311,7 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
     }
     // Epilogue: lane holds rows 4g..4g+3 of the wave's 16 (consecutive output
     // columns of one pair row) for token column lane%16 of each block.
-    const int c0 = blockIdx.y * kTileRows + wave * 16 + 4 * g;
+    const int c0 = rb * kTileRows + wave * 16 + 4 * g;
 #pragma unroll
     for (int b = 0; b < NTB; ++b) {
         const int j = 16 * b + (lane & 15);
@@ -302,14 +332,23 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
     }
 }
 
-// grid = (max_tiles, rows / 64), block = 256. TWO: stage A (W1 and W3, SwiGLU
+// grid = tiles8 * (rows / 64) (tiles8 = tiles rounded up to a multiple of
+// 8), block = 256. Workgroup L is taken as running on XCD L % 8 (the
+// dispatcher's round robin; only locality depends on it): the XCD's k-th
+// workgroup, k = L / 8, takes row block k % RB of tile 8 * (k / RB) + L % 8,
+// so one tile's row blocks run back to back on one XCD and share its L2
+// copy of the tile's activation rows. TWO: stage A (W1 and W3, SwiGLU
 // epilogue into M); otherwise stage B (W2, weighted fp32 rows into Y). The
 // tile's token-block count selects a specialised body.
 template <bool TWO>
-__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a, int RB) {
     __shared__ __align__(16) uint16_t xs[2][kTileTok * kLdsRow];   // 2 x 17 KB
+    __shared__ __align__(16) uint8_t sl[(TWO ? 2 : 1) * kTileRows * (kMaxRed / kBlk)];
     __shared__ int s_row[kTileTok];
-    const int ti = blockIdx.x;
+    const int L = blockIdx.x;
+    const int k = L >> 3;
+    const int rb = k % RB;
+    const int ti = 8 * (k / RB) + (L & 7);
     if (ti >= a.header[0]) return;                                  // whole workgroup
     const int t = threadIdx.x;
     const int e = a.tile_e[ti];
@@ -321,17 +360,17 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a) 
     }
     __syncthreads();
     const int S = a.K / kStep;
-#define DSV4_TILES(SV)                                                          \
-    switch ((n + 15) / 16) {                                                    \
-        case 1: prefill_gemm_tile<TWO, 1, SV>(a, e, p0, n, xs, s_row); break;  \
-        case 2: prefill_gemm_tile<TWO, 2, SV>(a, e, p0, n, xs, s_row); break;  \
-        case 3: prefill_gemm_tile<TWO, 3, SV>(a, e, p0, n, xs, s_row); break;  \
-        default: prefill_gemm_tile<TWO, 4, SV>(a, e, p0, n, xs, s_row); break; \
+#define DSV4_TILES(SV, DW)                                                                   \
+    switch ((n + 15) / 16) {                                                                 \
+        case 1: prefill_gemm_tile<TWO, 1, SV, DW>(a, e, p0, n, rb, xs, s_row, sl); break;  \
+        case 2: prefill_gemm_tile<TWO, 2, SV, DW>(a, e, p0, n, rb, xs, s_row, sl); break;  \
+        case 3: prefill_gemm_tile<TWO, 3, SV, DW>(a, e, p0, n, rb, xs, s_row, sl); break;  \
+        default: prefill_gemm_tile<TWO, 4, SV, DW>(a, e, p0, n, rb, xs, s_row, sl); break; \
     }
-    if (S == 32) { DSV4_TILES(32) }
-    else if (S == 16) { DSV4_TILES(16) }
-    else if (S == 4) { DSV4_TILES(4) }
-    else { DSV4_TILES(0) }
+    if (S == 32) { DSV4_TILES(32, kDWDeep) }
+    else if (S == 16) { DSV4_TILES(16, kDWDeep) }
+    else if (S == 4) { DSV4_TILES(4, kDepth) }
+    else { DSV4_TILES(0, kDepth) }
 #undef DSV4_TILES
 }
 
@@ -474,8 +513,9 @@ extern "C" int mxfp4_moe_prefill(const dsv4_bf16_t* x, const uint8_t* W1_packed,
     A.pair_tok = pt.pair_tok;
     A.pair_w = pt.pair_w;
     A.M = M;
-    hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3((unsigned)L.max_tiles, (unsigned)(hidden / kTileRows)),
-                       dim3(256), 0, stream, A);
+    const unsigned tiles8 = (unsigned)((L.max_tiles + 7) / 8 * 8);
+    hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(tiles8 * (unsigned)(hidden / kTileRows)), dim3(256), 0,
+                       stream, A, hidden / kTileRows);
     if (hipGetLastError() != hipSuccess) return -6;
 
     GemmArgs B = A;
@@ -492,8 +532,8 @@ extern "C" int mxfp4_moe_prefill(const dsv4_bf16_t* x, const uint8_t* W1_packed,
     B.rows = out_dim;
     B.M = nullptr;
     B.Y = Y;
-    hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3((unsigned)L.max_tiles, (unsigned)(out_dim / kTileRows)),
-                       dim3(256), 0, stream, B);
+    hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(tiles8 * (unsigned)(out_dim / kTileRows)), dim3(256), 0,
+                       stream, B, out_dim / kTileRows);
     if (hipGetLastError() != hipSuccess) return -7;
 
     hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)T, (unsigned)((out_dim / 4 + 255) / 256)),
