@@ -870,6 +870,86 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
     }
 }
 
+// One token (T = 1) with whole 16-row tiles, 16-byte aligned scales and at
+// most WB expert slots: the one-token path of moe_down_kernel as a kernel of
+// its own (no other path shares its registers or code). Wave w takes slot
+// w: its table reads are unconditional (slot_info_t1_wave); its M slice, then
+// its RB scale rows (one load of RB*NBB bytes per lane, spread through the
+// wave's LDS slot), then its W2 rows are issued, so the dots start as soon as
+// the first row arrives. No branch surrounds a load. Slots past the routed
+// ones load a valid expert's rows and contribute 0. The RB row sums of the
+// WB waves meet in LDS and are added in wave order, then rounded to bf16.
+template <int NBB, int RB, int WB, bool INDEXED, int BD>
+__global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_t1_kernel(const StageBArgs a) {
+    __shared__ float acc[WB][RB];
+    __shared__ __align__(16) uint8_t sstage[WB][RB * 64 * NBB];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int o0 = blockIdx.x * RB;
+    const int nblk = a.hidden / kBlkElems;
+    const int64_t wrow = a.hidden / 2;
+    const int b0 = NBB * lane;
+    int expert, pbeg;
+    float wt;
+    bool valid;
+    slot_info_t1_wave<INDEXED>(a.es, wave, lane, expert, pbeg, wt, valid);
+    uint32_t ms[NBB][16];
+#pragma unroll
+    for (int j = 0; j < NBB; ++j)
+        load_act_block<true>(a.M + (int64_t)pbeg * a.hidden + (b0 + j) * kBlkElems, ms[j]);
+    const uint8_t* W2 = a.w2 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* S2 = a.s2 + (int64_t)expert * a.s_exp_stride;
+    using SPiece = typename ScalePiece<RB * NBB>::type;
+    const SPiece spiece = *reinterpret_cast<const SPiece*>(S2 + (int64_t)o0 * nblk + lane * (RB * NBB));
+    __builtin_amdgcn_sched_barrier(0);  // keep the M and scale loads oldest
+    u32x4 w[RB][NBB];
+    auto load_row = [&](int r) {
+#pragma unroll
+        for (int j = 0; j < NBB; ++j)
+            w[r][j] = ld16_stream(W2 + (int64_t)(o0 + r) * wrow + (int64_t)(b0 + j) * 16);
+    };
+#pragma unroll
+    for (int r = 0; r < BD; ++r) load_row(r);
+    reinterpret_cast<SPiece*>(&sstage[wave][0])[lane] = spiece;
+    __builtin_amdgcn_wave_barrier();
+    uint32_t sc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int j = 0; j < NBB; ++j) v |= (uint32_t)sstage[wave][r * nblk + b0 + j] << (8 * j);
+        sc[r] = v;
+    }
+    float part[RB];
+    float chain = 0.f;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < NBB; ++j) {
+            reg_barrier_after(w[r][j], chain);
+            sum = fmaf(fp4_block_dot(w[r][j], ms[j]), scale_of(sc[r], j), sum);
+            chain = sum;
+        }
+        part[r] = sum;
+        if (r + BD < RB) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_row(r + BD);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    wave_reduce_n<RB>(part, lane);
+    const int r = reduced_index<RB>(lane);
+    if (reduced_owner<RB>(lane)) acc[wave][r] = valid ? wt * part[0] : 0.f;
+    __syncthreads();
+    if (threadIdx.x < RB) {
+        float sum = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < WB; ++w2) sum += acc[w2][threadIdx.x];
+        a.out[o0 + threadIdx.x] = f32_to_bf16_bits(sum);
+    }
+}
+
 // ------------------------------------------------------------ routing ------
 
 
@@ -1157,6 +1237,17 @@ hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
     // 16), 16-byte aligned scales (staged with one load per lane) and at most
     // one expert slot per wave (8 waves).
     a.stage_scales = !MULTI && a.out_dim % 16 == 0 && aligned16(a.s2) && a.es.n_slots <= 8;
+    // One token with the default shapes: the dedicated one-token kernel.
+    if (TMAX == 1 && fast && a.stage_scales && (nb == 1 || nb == 2) && sh.rb == 8 && sh.wb == 8 &&
+        !sh.bpipe && sh.b1_depth >= 8) {
+        if (nb == 1)
+            hipLaunchKernelGGL((moe_down_t1_kernel<1, 8, 8, INDEXED, 8>), dim3((unsigned)(a.out_dim / 8)),
+                               dim3(64 * 8), 0, stream, a);
+        else
+            hipLaunchKernelGGL((moe_down_t1_kernel<2, 8, 8, INDEXED, 8>), dim3((unsigned)(a.out_dim / 8)),
+                               dim3(64 * 8), 0, stream, a);
+        return hipGetLastError();
+    }
 #define DSV4_B(NBV, RBV, WBV, FASTV, PIPEV)                                                        \
     hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, FASTV, PIPEV, MULTI>),       \
                        dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
