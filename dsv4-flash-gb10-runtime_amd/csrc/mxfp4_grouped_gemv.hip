@@ -272,11 +272,15 @@ struct RouteTables {
 // One-token gating folded into stage A (mxfp4_moe_layer at T = 1): every
 // workgroup computes the top-k of the logits itself and workgroup (0, 0)
 // publishes ids, weights and the routing tables stage B reads.
+// One-token routing inside stage A: from logits (the config gating), or
+// from the caller's ids and weights (what the routing kernel would build).
 struct GateArgs {
-    const float* logits;        // [n_experts] fp32
+    const float* logits;        // [n_experts] fp32, or null when ids are given
+    const int32_t* ids_in;      // [topk] given expert ids (logits == null)
+    const float* w_in;          // [topk] given weights
     int n_experts;
     int topk;
-    int32_t* ids_out;           // [topk] or null
+    int32_t* ids_out;           // [topk] or null (logits only)
     float* w_out;               // [topk] or null
     RouteTables rt;
 };
@@ -479,7 +483,9 @@ __global__ __launch_bounds__(64 * kWavesA, PIPE ? 1 : 4) void moe_swiglu_kernel(
 // only then writes activation and scales to LDS: the wait covers the oldest
 // loads only, so the weight stream starts at once. Rows past `hidden` and
 // unrouted slots are loaded but not stored.
-template <int NB, int HC, bool INDEXED, int kT1Waves, int D, bool GATE>
+// GATE: 0 = routing tables given (the routing kernel ran); 1 = rank the
+// logits; 2 = the caller's ids and weights.
+template <int NB, int HC, bool INDEXED, int kT1Waves, int D, int GATE>
 __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const StageAArgs a) {
     constexpr int kThreads = 64 * kT1Waves;
     constexpr int kRows = kT1Waves * HC;
@@ -489,6 +495,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     __shared__ u32x4 xl[kMaxRed * 2 / 16];
     __shared__ u32x4 sl[kSTile / 16];
     __shared__ int s_pick[GATE ? kMaxTopk : 1];
+    __shared__ int s_nu[1];
     const uint8_t* slb = reinterpret_cast<const uint8_t*>(sl);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -508,7 +515,56 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
 
     int expert, pbeg;
     bool valid;
-    if constexpr (GATE) {
+    if constexpr (GATE == 2) {
+        // Wave 0 forms the slots the routing kernel would (the same
+        // computation in every workgroup): the distinct in-range ids in
+        // ascending order, each with the summed weight of its listings (in
+        // listing order). Workgroup (0, 0) publishes them for stage B.
+        if (wave == 0) {
+            const GateArgs& g = a.gate;
+            const int k = min(lane, g.topk - 1);
+            const int e = g.ids_in[k];
+            const float wl = g.w_in[k];
+            const bool listed = lane < g.topk;
+            bool first = true;
+            float wsum = 0.f;
+            for (int j = 0; j < g.topk; ++j) {
+                const int ej = __builtin_amdgcn_readlane(e, j);
+                const float wj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wl), j));
+                first = first && !(j < lane && ej == e);
+                wsum += (ej == e) ? wj : 0.f;
+            }
+            const bool take = listed && first && e >= 0 && e < g.n_experts;
+            const uint64_t tk = __ballot(take);
+            const int U = __builtin_popcountll(tk);
+            int rank = 0;
+            for (int j = 0; j < g.topk; ++j) {
+                const int ej = __builtin_amdgcn_readlane(e, j);
+                rank += ((tk >> j) & 1) && ej < e;
+            }
+            if (take) s_pick[rank] = e;
+            if (lane >= U && lane < a.es.n_slots) s_pick[lane] = 0;   // valid id for addresses
+            if (lane == 0) s_nu[0] = U;
+            if (blockIdx.x == 0 && blockIdx.y == 0) {
+                if (take) {
+                    g.rt.uexp[rank] = e;
+                    g.rt.off[rank] = rank;
+                    g.rt.pair_tok[rank] = 0;
+                    g.rt.pair_w[rank] = wsum;
+                }
+                if (lane >= U && lane < g.rt.n_slots) g.rt.uexp[lane] = 0;
+                if (lane == 0) {
+                    g.rt.header[0] = U;
+                    g.rt.header[1] = U;
+                    g.rt.off[U] = U;
+                }
+            }
+        }
+        __syncthreads();
+        expert = s_pick[blockIdx.y];
+        pbeg = blockIdx.y;
+        valid = (int)blockIdx.y < s_nu[0];
+    } else if constexpr (GATE == 1) {
         // Wave 0 ranks the logits (the same computation in every workgroup);
         // workgroup (0, 0) publishes the routing for stage B and the caller.
         if (wave == 0) {
@@ -1178,9 +1234,10 @@ bool stage_a_t1_ok(const StageAArgs& a, bool aligned) {
            aligned16(a.s3);
 }
 
-// gate: the one-token kernel also ranks a.gate.logits (requires stage_a_t1_ok).
+// gate: the one-token kernel also routes (1: ranks a.gate.logits; 2: takes
+// a.gate.ids_in / w_in); requires stage_a_t1_ok.
 template <bool INDEXED, bool ALIGNED, bool MULTI>
-hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, bool gate = false) {
+hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, int gate = 0) {
     const Shapes& sh = shapes();
     const int nb = blocks_per_lane(a.K);
     a.scale_vec = scale_vec_ok(nb, a.K / kBlkElems, a.s1, a.s3);
@@ -1200,10 +1257,12 @@ hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, bool gate
     if (gate && !(t1 && INDEXED)) return hipErrorInvalidValue;
     if (t1) {
         dim3 g1((unsigned)(a.hidden / (W * 4)), (unsigned)slots);
-#define DSV4_T1(NBV, WV)                                                                                       \
-    if (gate) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED>), g1, dim3(64 * WV), 0, \
-                                 stream, a);                                                                   \
-    else hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, false>), g1, dim3(64 * WV), 0, stream, a);
+#define DSV4_T1(NBV, WV)                                                                                   \
+    if (gate == 1) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED ? 1 : 0>), g1,  \
+                                      dim3(64 * WV), 0, stream, a);                                         \
+    else if (gate == 2) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED ? 2 : 0>), \
+                                           g1, dim3(64 * WV), 0, stream, a);                                \
+    else hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, 0>), g1, dim3(64 * WV), 0, stream, a);
         if (nb == 1) { DSV4_T1(1, 4) }
         else if (W == 4) { DSV4_T1(2, 4) }
         else if (W == 8) { DSV4_T1(2, 8) }
@@ -1378,7 +1437,7 @@ int launch_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed, const uint8_t*
     hipError_t e;
     if (gate != nullptr) {
         A.gate = *gate;
-        e = launch_stage_a<true, true, false>(A, c.es.n_slots, stream, true);
+        e = launch_stage_a<true, true, false>(A, c.es.n_slots, stream, gate->logits != nullptr ? 1 : 2);
     } else if (T == 1)
         e = al ? launch_stage_a<true, true, false>(A, c.es.n_slots, stream)
                : launch_stage_a<true, false, false>(A, c.es.n_slots, stream);
@@ -1575,6 +1634,23 @@ extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_pa
     int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
     if (v != 0) return v;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
+    if (T == 1) {
+        // One token: stage A forms the slots from the ids itself (two
+        // launches in all; the same slots, weights and results as the
+        // routing kernel's).
+        StageAArgs probe{};
+        probe.K = K_in;
+        probe.hidden = hidden;
+        probe.s1 = W1_scale;
+        probe.s3 = W3_scale;
+        const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
+        if (stage_a_t1_ok(probe, al)) {
+            GateArgs g{nullptr, ids, weights, n_experts, topk, nullptr, nullptr, c.rt};
+            v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
+            if (v != 0) return v;
+            return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+        }
+    }
     v = launch_route(nullptr, ids, weights, T, topk, n_experts, nullptr, nullptr, c, stream);
     if (v != 0) return v;
     v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
@@ -1602,7 +1678,7 @@ extern "C" int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
         probe.s3 = W3_scale;
         const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
         if (stage_a_t1_ok(probe, al)) {
-            GateArgs g{logits, n_experts, topk, ids_out, weights_out, c.rt};
+            GateArgs g{logits, nullptr, nullptr, n_experts, topk, ids_out, weights_out, c.rt};
             v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
             if (v != 0) return v;
             return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);

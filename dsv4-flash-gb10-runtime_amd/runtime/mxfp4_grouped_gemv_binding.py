@@ -342,9 +342,11 @@ def mxfp4_moe_layer(
 
 
 class MoEStages:
-    """The three launches of mxfp4_moe_grouped_gemv, callable one by one on a
-    fixed workspace (preallocated here): build_routing(ids, weights) ->
-    swiglu(x) -> down(out)."""
+    """The three launches of the general mxfp4_moe_grouped_gemv path (routing
+    kernel, stage A, stage B), callable one by one on a fixed workspace
+    (preallocated here): build_routing(ids, weights) -> swiglu(x) -> down(out).
+    At T = 1 mxfp4_moe_grouped_gemv itself runs two launches (stage A forms the
+    routing) with the same results."""
 
     def __init__(self, W1, W3, W2, T: int, topk: int, device):
         self.lib = _load_lib()

@@ -303,6 +303,37 @@ def test_moe_duplicate_and_out_of_range_ids(device):
     assert_close(host_bits(out1), host_bits(out)[:1], "duplicate merge", cos_tol=0.99999)
 
 
+@pytest.mark.parametrize("ids_row", [[3, 5, 1, 7, 12, 0, 9, 14], [3, 3, 5, 15, 3, 8, 8, 1],
+                                     [-1, 2, 16, 2, 1000, -7, 4, 2], [6, 6, 6, 6, 6, 6, 6, 6]],
+                         ids=["distinct", "duplicates", "invalid-and-duplicates", "one-expert"])
+def test_moe_one_token_ids_path(device, ids_row):
+    """At T = 1 mxfp4_moe_grouped_gemv forms the routing inside stage A (two
+    launches). Its slots (distinct in-range ids, ascending, summed weights of
+    repeated listings) and results must equal the routing kernel's path
+    (build_routing + swiglu + down) bit for bit, and the oracle."""
+    E, K, H, O, topk = 16, 2048, 256, 256, 8
+    announce(f"mxfp4_moe_grouped_gemv T=1 ids path {ids_row}")
+    W1p, W1s = synth.mxfp4_weight(8400, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8404, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8408, O, H, E)
+    x = synth.normal_bf16(8410, (1, K))
+    ids = np.array([ids_row], np.int32)
+    w = (np.arange(1, topk + 1, dtype=np.float32) / 36.0).reshape(1, topk)
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    ids_d, w_d, x_d = torch.from_numpy(ids).to(device), dev_f32(w, device), dev_bf16(x, device)
+    out = host_bits(gb.mxfp4_moe_grouped_gemv(x_d, W1, W3, W2, ids_d, w_d))
+    st = gb.MoEStages(W1, W3, W2, 1, topk, device)
+    st.build_routing(ids_d, w_d)
+    st.swiglu(x_d)
+    ref_path = host_bits(st.down(torch.empty(1, O, dtype=torch.bfloat16, device=device)))
+    assert np.array_equal(out, ref_path), "T=1 ids path differs from the routing-kernel path"
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    assert_close(out, mx.moe_layer(x, fn, ids, w, O, n_experts=E), "T=1 ids path vs oracle")
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_indexed_config_dims(device, T):
     """Config-3 shapes (256 experts, K=4096, H=2048, O=4096) with device-filled weights."""
