@@ -231,6 +231,35 @@ def moe_layer(x, expert_fn, ids, weights, out_dim: int, n_experts=None) -> np.nd
     return bf16_round(acc)
 
 
+def dequant_expert_f32(expert):
+    """((W1p, W1s), (W3p, W3s), (W2p, W2s)) -> (W1, W3, W2) as fp32 arrays of the
+    bf16 dequantised weights, the form moe_layer_dequantised takes."""
+    return tuple(bf16_to_f32(mxfp4_dequant_bf16(p, s)) for p, s in expert)
+
+
+def moe_layer_dequantised(x, dq_fn, ids, weights, out_dim: int) -> np.ndarray:
+    """moe_layer with the dequantisation hoisted out of the call: dq_fn(e) returns
+    the expert's (W1, W3, W2) already dequantised (dequant_expert_f32). Same
+    arithmetic and order as moe_layer, so the results are bit-identical; it
+    times the matmuls alone, the "weights dequantised ahead of time" host path
+    (runtime/mxfp4_loader.py:272-309 dequantises once at load time)."""
+    x = np.atleast_2d(np.asarray(x, dtype=np.uint16))
+    xf = bf16_to_f32(x)
+    ids = np.asarray(ids)
+    weights = np.asarray(weights, dtype=np.float32)
+    acc = np.zeros((x.shape[0], out_dim), dtype=np.float32)
+    for e in np.unique(ids):
+        tok, kk = np.nonzero(ids == e)
+        W1, W3, W2 = dq_fn(int(e))
+        g = (xf[tok] @ W1.T).astype(np.float32)
+        u = (xf[tok] @ W3.T).astype(np.float32)
+        M = bf16_round(silu_f32(g) * u)
+        y = (bf16_to_f32(M) @ W2.T).astype(np.float32)
+        for i, t in enumerate(tok):
+            acc[t] = (acc[t] + weights[t, kk[i]] * y[i]).astype(np.float32)
+    return bf16_round(acc)
+
+
 def route_sigmoid_topk(logits, topk: int):
     """Config gating: top-k logits per token (descending, ties to the lower
     index), weights sigmoid(l) / sum sigmoid over the top-k. The reference's own

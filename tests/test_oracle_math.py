@@ -152,6 +152,23 @@ def test_moe_layer_equals_per_token_grouped():
         assert rel < 1e-3 and cos > 0.99999
 
 
+def test_moe_layer_dequantised_is_bit_identical():
+    K, H, O, E, T, topk = 128, 64, 64, 12, 3, 4
+    W1p, W3p, W2p, W1s, W3s, W2s = _experts(39, E, K, H, O)
+    x = synth.normal_bf16(40, (T, K))
+    ids, w = mx.route_sigmoid_topk(synth.gating_logits(41, T, E), topk)
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    out = mx.moe_layer(x, fn, ids, w, O)
+    pre = {e: mx.dequant_expert_f32(fn(e)) for e in range(E)}
+    assert np.array_equal(mx.moe_layer_dequantised(x, pre.__getitem__, ids, w, O), out)
+    # the dequantised W1 of expert 0 against the dense GEMV oracle
+    y = mx.bf16_round(mx.bf16_to_f32(x) @ pre[0][0].T)
+    assert np.array_equal(y, mx.mxfp4_gemv(x, W1p[0], W1s[0]))
+
+
 def test_route_matches_torch():
     logits = synth.gating_logits(37, 16, 256)
     ids, w = mx.route_sigmoid_topk(logits, 8)
