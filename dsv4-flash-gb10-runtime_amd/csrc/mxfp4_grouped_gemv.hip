@@ -689,6 +689,171 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         a.M[(int64_t)pbeg * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
 }
 
+// Several tokens (T > 1, expert-indexed routing tables) on the FAST path: the
+// one-token kernel's layout with the expert's pairs looped over. A workgroup
+// of kTNWaves waves covers R = kTNWaves*HC rows of one unique expert; each
+// wave loads its HC rows of W1 and W3 once (lane l owns MX blocks l, l+64, so
+// each load instruction reads one KiB of a row) and reduces them against the
+// activation of every token that the expert serves. The loads depend on the
+// routing tables (slot -> pairs -> tokens) and are issued in that order:
+// tables, then the first pair's activation and the workgroup's scale tile,
+// then the weight rows, so that waiting for the activation never waits for a
+// weight row. Further pairs (an expert routed by several tokens) are staged
+// TT at a time once the first pair's dots are done, while the weight rows
+// stay in registers.
+template <int NB, int HC, int kTNWaves, int TT>
+__global__ __launch_bounds__(64 * kTNWaves, 4) void moe_swiglu_tn_kernel(const StageAArgs a) {
+    constexpr int kThreads = 64 * kTNWaves;
+    constexpr int kRows = kTNWaves * HC;
+    constexpr int kXSlot = kMaxRed / 8;                                  // 16-byte pieces per staged activation
+    constexpr int kX1 = (kXSlot + kThreads - 1) / kThreads;              // pieces per thread, one activation
+    constexpr int kXPer = (TT * kXSlot + kThreads - 1) / kThreads;       // pieces per thread, TT activations
+    constexpr int kSTile = 2 * kRows * (kMaxRed / kBlkElems);
+    constexpr int kSPer = (kSTile / 16 + kThreads - 1) / kThreads;
+    __shared__ u32x4 xl[TT * kXSlot];
+    __shared__ u32x4 sl[kSTile / 16];
+    const uint8_t* slb = reinterpret_cast<const uint8_t*>(sl);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int hw = blockIdx.x * kRows;
+    const int h0 = hw + wave * HC;
+    const int K = a.K;
+    const int nblk = K / kBlkElems;
+    const int64_t wrow = K / 2;
+    const int nx = K / 8;                      // 16-byte pieces of one token's activation
+    const int ns = kRows * nblk / 16;
+
+    const ExpertSet& es = a.es;
+    const int y = blockIdx.y;
+    const int U = *es.n_unique;
+    const int e_raw = es.uexp[y];
+    const int pbeg = es.off[y];
+    const int pend = es.off[y + 1];
+    if (y >= U) return;
+    const int expert = min(max(e_raw, 0), es.n_experts - 1);
+
+    const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);
+    // The first pair's activation into LDS slot 0.
+    u32x4 x1[kX1];
+    {
+        const int tok = es.pair_tok[pbeg];
+#pragma unroll
+        for (int i = 0; i < kX1; ++i)
+            x1[i] = xg[(int64_t)tok * nx + min((int)threadIdx.x + kThreads * i, nx - 1)];
+    }
+
+    const uint8_t* W1 = a.w1 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* W3 = a.w3 + (int64_t)expert * a.w_exp_stride;
+    const uint8_t* S1 = a.s1 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
+    const uint8_t* S3 = a.s3 + (int64_t)expert * a.s_exp_stride + (int64_t)hw * nblk;
+    u32x4 sv[kSPer];
+#pragma unroll
+    for (int i = 0; i < kSPer; ++i) {
+        const int t = min((int)threadIdx.x + kThreads * i, 2 * ns - 1);
+        const uint8_t* src = t < ns ? S1 + 16 * t : S3 + 16 * (t - ns);
+        sv[i] = *reinterpret_cast<const u32x4*>(src);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // activations and scales before the weights
+
+    // Weights in the order the dots consume them: block pass j of every row,
+    // then pass j+1.
+    GateUpChunk<NB, HC> c;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+#pragma unroll
+        for (int r = 0; r < HC; ++r) {
+            const int64_t wo = (int64_t)(h0 + r) * wrow + (int64_t)(lane + 64 * j) * 16;
+            c.w1[r][j] = ld16_stream(W1 + wo);
+            c.w3[r][j] = ld16_stream(W3 + wo);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kX1; ++i) {
+        const int idx = threadIdx.x + kThreads * i;
+        if (idx < nx) xl[idx] = x1[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kSPer; ++i) {
+        const int idx = threadIdx.x + kThreads * i;
+        if (idx < 2 * ns) sl[idx] = sv[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < HC; ++r) {
+        const int row = wave * HC + r;
+        uint32_t p1 = 0, p3 = 0;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            p1 |= (uint32_t)slb[row * nblk + lane + 64 * j] << (8 * j);
+            p3 |= (uint32_t)slb[kRows * nblk + row * nblk + lane + 64 * j] << (8 * j);
+        }
+        c.s1[r] = p1;
+        c.s3[r] = p3;
+    }
+
+    // Dots of the wave's rows against staged activation tt, stored as M of
+    // pair p. Block pass j of all rows, then pass j+1: only pass j's slice of
+    // the activation is in registers, and each row still adds its blocks in
+    // ascending order.
+    auto emit = [&](int tt, int p) {
+        float g[HC], u[HC];
+#pragma unroll
+        for (int r = 0; r < HC; ++r) g[r] = u[r] = 0.f;
+        float chain = 0.f;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            uint32_t xs[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x4 v = xl[tt * kXSlot + (lane + 64 * j) * 4 + q];
+                xs[4 * q + 0] = v[0];
+                xs[4 * q + 1] = v[1];
+                xs[4 * q + 2] = v[2];
+                xs[4 * q + 3] = v[3];
+            }
+#pragma unroll
+            for (int r = 0; r < HC; ++r) {
+                reg_barrier_after(c.w1[r][j], chain);
+                g[r] = fmaf(fp4_block_dot(c.w1[r][j], xs), scale_of(c.s1[r], j), g[r]);
+                reg_barrier_after(c.w3[r][j], g[r]);
+                u[r] = fmaf(fp4_block_dot(c.w3[r][j], xs), scale_of(c.s3[r], j), u[r]);
+                chain = u[r];
+            }
+        }
+        wave_reduce_n<HC>(g, lane);
+        wave_reduce_n<HC>(u, lane);
+        const int r = reduced_index<HC>(lane);
+        if (reduced_owner<HC>(lane) && h0 + r < a.hidden)
+            a.M[(int64_t)p * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
+    };
+    // The first pair in straight-line code, so that each row's dots start as
+    // soon as that row has arrived.
+    emit(0, pbeg);
+    // Further pairs, TT at a time, against the rows still in registers.
+#pragma unroll 1
+    for (int pb = pbeg + 1; pb < pend; pb += TT) {
+        u32x4 xv[kXPer];
+#pragma unroll
+        for (int i = 0; i < kXPer; ++i) {
+            // pairs past pend repeat the last one: staged, never used
+            const int idx = min((int)threadIdx.x + kThreads * i, TT * nx - 1);
+            const int tt = idx / nx;
+            const int tok = es.pair_tok[min(pb + tt, pend - 1)];
+            xv[i] = xg[(int64_t)tok * nx + (idx - tt * nx)];
+        }
+        __syncthreads();  // every wave is done with the previous pass's slots
+#pragma unroll
+        for (int i = 0; i < kXPer; ++i) {
+            const int idx = threadIdx.x + kThreads * i;
+            if (idx < TT * nx) xl[(idx / nx) * kXSlot + idx % nx] = xv[i];
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int tt = 0; tt < min(TT, pend - pb); ++tt) emit(tt, pb + tt);
+    }
+}
+
 // ---------------------------------------------------------------- stage B --
 
 struct StageBArgs {
@@ -1006,6 +1171,126 @@ __global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_t1_kernel(c
     }
 }
 
+// Several tokens (T > 1, expert-indexed) on the FAST path with one MX block
+// per lane per row (hidden = 2048): moe_down_kernel's split of the work (a
+// workgroup owns RB output rows; wave w takes expert slots w, w+WB, ...) with
+// twice the bytes in flight per wave. Lane i of a wave first reads the
+// routing entries of the wave's slot i (expert, pair range, first pair's
+// token and weight: two round trips for all slots). Each step then issues
+// the loads of two slots at once (2*RB rows) and reduces them in order.
+// Further pairs of a slot (an expert routed by several tokens) load their M
+// slice on demand. Partial sums per (wave, token, row) meet in LDS and are
+// added in wave order, the order of moe_down_kernel, so the results are the
+// same bits.
+template <int RB, int WB, int TM>
+__global__ __launch_bounds__(64 * WB, 4) void moe_down_tn_kernel(const StageBArgs a) {
+    __shared__ float acc[WB][TM][RB];
+    __shared__ __align__(16) uint8_t sstage[WB][RB * 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int o0 = blockIdx.x * RB;
+    const int nblk = a.hidden / kBlkElems;     // 64
+    const int64_t wrow = a.hidden / 2;
+    const ExpertSet& es = a.es;
+    {
+        float* accf = &acc[0][0][0];
+        for (int i = threadIdx.x; i < WB * TM * RB; i += 64 * WB) accf[i] = 0.f;
+    }
+
+    const int U = min(*es.n_unique, es.n_slots);
+    const int ns = U > wave ? (U - wave + WB - 1) / WB : 0;  // this wave's slots (<= 64, host-checked)
+    const int su = min(wave + WB * lane, max(U - 1, 0));
+    const int e_l = min(max(es.uexp[su], 0), es.n_experts - 1);
+    const int pb_l = min(max(es.off[su], 0), es.n_pairs - 1);
+    const int pe_l = min(max(es.off[su + 1], pb_l + 1), es.n_pairs);
+    const int tok_l = min(max(es.pair_tok[pb_l], 0), a.T - 1);
+    const float w_l = es.pair_w[pb_l];
+    __syncthreads();  // acc zeroed
+
+    using SPiece = typename ScalePiece<RB>::type;
+    struct Rows {
+        u32x4 w[RB];
+        SPiece sp;
+    };
+    uint32_t m[16];  // the M slice of the pair being reduced (one at a time)
+    auto issue_rows = [&](int i, Rows& b) {
+        const int e = __builtin_amdgcn_readlane(e_l, i);
+        const uint8_t* W2 = a.w2 + (int64_t)e * a.w_exp_stride;
+        const uint8_t* S2 = a.s2 + (int64_t)e * a.s_exp_stride;
+        b.sp = *reinterpret_cast<const SPiece*>(S2 + (int64_t)o0 * nblk + lane * RB);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) b.w[r] = ld16_stream(W2 + (int64_t)(o0 + r) * wrow + lane * 16);
+    };
+    auto load_m = [&](int p) { load_act_block<true>(a.M + (int64_t)p * a.hidden + lane * kBlkElems, m); };
+    // Row r's scale byte for this lane's block is read from the wave's LDS
+    // slot where it is used. The barrier applies to the rows' own registers:
+    // a copy would make the compiler wait for a row early.
+    auto dots = [&](Rows& b, int tok, float wt) {
+        float part[RB];
+        float chain = 0.f;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            reg_barrier_after(b.w[r], chain);
+            part[r] = fmaf(fp4_block_dot(b.w[r], m), scale_of(sstage[wave][r * nblk + lane], 0), 0.f);
+            chain = part[r];
+        }
+        wave_reduce_n<RB>(part, lane);
+        const int r = reduced_index<RB>(lane);
+        if (reduced_owner<RB>(lane)) acc[wave][tok][r] += wt * part[0];
+    };
+    // Slot i with its first pair's M slice already loaded.
+    auto process = [&](int i, Rows& b) {
+        reinterpret_cast<SPiece*>(&sstage[wave][0])[lane] = b.sp;
+        __builtin_amdgcn_wave_barrier();
+        dots(b, __builtin_amdgcn_readlane(tok_l, i),
+             __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w_l), i)));
+        const int p0 = __builtin_amdgcn_readlane(pb_l, i);
+        const int p1 = __builtin_amdgcn_readlane(pe_l, i);
+#pragma unroll 1
+        for (int p = p0 + 1; p < p1; ++p) {
+            const int tok = min(max(es.pair_tok[p], 0), a.T - 1);
+            const float wt = es.pair_w[p];
+            load_m(p);
+            dots(b, tok, wt);
+        }
+    };
+
+    // Two slots per step: the first slot's M slice, both slots' scale bytes
+    // and rows, then the first slot is reduced (waiting for its own loads
+    // only), then the second slot's M slice (an L2 hit, written by stage A)
+    // is loaded into the same registers and the second slot is reduced.
+    // Every path through the loop consumes both row buffers; an odd last
+    // slot is reduced after the loop.
+    int i = 0;
+#pragma unroll 1
+    for (; i + 1 < ns; i += 2) {
+        Rows b0, b1;
+        load_m(__builtin_amdgcn_readlane(pb_l, i));
+        issue_rows(i, b0);
+        issue_rows(i + 1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        process(i, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_m(__builtin_amdgcn_readlane(pb_l, i + 1));
+        process(i + 1, b1);
+    }
+    if (i < ns) {
+        Rows b0;
+        load_m(__builtin_amdgcn_readlane(pb_l, i));
+        issue_rows(i, b0);
+        process(i, b0);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.T * RB; i += 64 * WB) {
+        const int t = i / RB;
+        const int r = i % RB;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < WB; ++w) sum += acc[w][t][r];
+        a.out[(int64_t)t * a.out_dim + o0 + r] = f32_to_bf16_bits(sum);
+    }
+}
+
 // ------------------------------------------------------------ routing ------
 
 
@@ -1180,6 +1465,8 @@ struct Shapes {
     int hc, pipe, h_per_wave;
     int rb, wb, bpipe;
     int t1, t1_waves, b1_depth;
+    int tn;                     // activations staged per pass by the multi-token kernel (0: generic kernel)
+    int tnb;                    // multi-token stage B: pipelined kernel (1) or generic (0)
 };
 
 const Shapes& shapes() {
@@ -1201,6 +1488,14 @@ const Shapes& shapes() {
         if (std::getenv("DSV4_GROUPED_T1") && std::atoi(std::getenv("DSV4_GROUPED_T1")) == 0) v.t1 = 0;
         // Rows in flight before the first dot of one-token stage B (of 8).
         v.b1_depth = env_int("DSV4_GROUPED_B1_DEPTH", 8);
+        // Multi-token stage A: DSV4_GROUPED_TN = activations staged per pass
+        // (1 or 2; 0 selects the generic kernel).
+        const char* tn_env = std::getenv("DSV4_GROUPED_TN");
+        const int tn = tn_env ? std::atoi(tn_env) : 2;
+        v.tn = tn >= 2 ? 2 : (tn >= 1 ? 1 : 0);
+        // Multi-token stage B: DSV4_GROUPED_TNB = 0 selects the generic kernel.
+        const char* tnb_env = std::getenv("DSV4_GROUPED_TNB");
+        v.tnb = tnb_env ? (std::atoi(tnb_env) != 0) : 1;
         return v;
     }();
     return s;
@@ -1255,7 +1550,19 @@ hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, int gate 
     const int W = nb == 1 ? 4 : sh.t1_waves;
     const bool t1 = !MULTI && stage_a_t1_ok(a, ALIGNED);
     if (gate && !(t1 && INDEXED)) return hipErrorInvalidValue;
-    if (t1) {
+    // Several tokens on the FAST path: the multi-token kernel (whole tiles of
+    // 16 rows, 16-byte aligned scale rows).
+    const bool tn = MULTI && INDEXED && fast && nb <= 2 && sh.tn > 0 && a.hidden % 16 == 0 &&
+                    aligned16(a.s1) && aligned16(a.s3);
+    if (tn) {
+        dim3 gn((unsigned)(a.hidden / 16), (unsigned)slots);
+#define DSV4_TN(NBV)                                                                                    \
+    if (sh.tn == 2) hipLaunchKernelGGL((moe_swiglu_tn_kernel<NBV, 4, 4, 2>), gn, dim3(256), 0, stream, a); \
+    else hipLaunchKernelGGL((moe_swiglu_tn_kernel<NBV, 4, 4, 1>), gn, dim3(256), 0, stream, a);
+        if (nb == 1) { DSV4_TN(1) }
+        else { DSV4_TN(2) }
+#undef DSV4_TN
+    } else if (t1) {
         dim3 g1((unsigned)(a.hidden / (W * 4)), (unsigned)slots);
 #define DSV4_T1(NBV, WV)                                                                                   \
     if (gate == 1) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED ? 1 : 0>), g1,  \
@@ -1304,6 +1611,18 @@ hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
                                dim3(64 * 8), 0, stream, a);
         else
             hipLaunchKernelGGL((moe_down_t1_kernel<2, 8, 8, INDEXED, 8>), dim3((unsigned)(a.out_dim / 8)),
+                               dim3(64 * 8), 0, stream, a);
+        return hipGetLastError();
+    }
+    // Several tokens, one block per lane per row, whole 8-row tiles, at most
+    // 64 slots per wave: the pipelined multi-token kernel.
+    if (MULTI && INDEXED && fast && nb == 1 && sh.tnb && a.out_dim % 8 == 0 && aligned16(a.s2) &&
+        a.es.n_slots <= 64 * 8 && a.T <= kMaxTokens) {
+        if (a.T <= 16)
+            hipLaunchKernelGGL((moe_down_tn_kernel<8, 8, 16>), dim3((unsigned)(a.out_dim / 8)), dim3(64 * 8), 0,
+                               stream, a);
+        else
+            hipLaunchKernelGGL((moe_down_tn_kernel<8, 8, kMaxTokens>), dim3((unsigned)(a.out_dim / 8)),
                                dim3(64 * 8), 0, stream, a);
         return hipGetLastError();
     }

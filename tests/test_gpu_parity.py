@@ -334,6 +334,44 @@ def test_moe_one_token_ids_path(device, ids_row):
     assert_close(out, mx.moe_layer(x, fn, ids, w, O, n_experts=E), "T=1 ids path vs oracle")
 
 
+@pytest.mark.parametrize("K,routing", [(2048, "random"), (4096, "random"), (4096, "shared"),
+                                       (2048, "ragged")])
+def test_moe_multi_token_many_pairs_per_expert(device, K, routing):
+    """Several tokens on the aligned path (K = 2048 or 4096, hidden = 2048) with
+    16 experts, so each expert serves many tokens: the multi-token stage A
+    stages the pairs after the first in passes, and the multi-token stage B
+    loads their M slices on demand. "shared": every token routes to the same
+    8 experts (16 pairs each); "ragged": 1 to 16 pairs per expert."""
+    E, H, O, T, topk = 16, 2048, 256, 16, 8
+    announce(f"mxfp4_moe_grouped_gemv T={T} E={E} K={K} routing={routing}")
+    W1p, W1s = synth.mxfp4_weight(8500, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8504, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8508, O, H, E)
+    x = synth.normal_bf16(8510 + K, (T, K))
+    if routing == "random":
+        ids, w = mx.route_sigmoid_topk(synth.gating_logits(8520 + K, T, E), topk)
+    else:
+        if routing == "shared":
+            ids = np.tile(np.array([2, 5, 7, 11, 0, 15, 9, 4], np.int32), (T, 1))
+        else:  # expert e < 8 taken by tokens t >= 2e, the rest fill each row
+            ids = np.zeros((T, topk), np.int32)
+            for t in range(T):
+                hot = [e for e in range(8) if t >= 2 * e]
+                cold = [8 + (t + i) % 8 for i in range(topk - len(hot))]
+                ids[t] = hot + cold
+        rng = np.random.default_rng(8530)
+        w = rng.random((T, topk)).astype(np.float32)
+        w /= w.sum(1, keepdims=True)
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    out = gb.mxfp4_moe_grouped_gemv(dev_bf16(x, device), W1, W3, W2,
+                                    torch.from_numpy(ids).to(device), dev_f32(w, device))
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    assert_close(host_bits(out), mx.moe_layer(x, fn, ids, w, O), f"moe T={T} K={K} {routing}")
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_indexed_config_dims(device, T):
     """Config-3 shapes (256 experts, K=4096, H=2048, O=4096) with device-filled weights."""
