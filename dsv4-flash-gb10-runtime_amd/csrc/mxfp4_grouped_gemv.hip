@@ -1294,12 +1294,12 @@ __global__ __launch_bounds__(64 * WB, 4) void moe_down_tn_kernel(const StageBArg
 // ------------------------------------------------------------ routing ------
 
 
-constexpr int kRouteThreads = 256;
-constexpr int kExpPerThread = kMaxExperts / kRouteThreads;  // 4
+constexpr int kRouteThreads = 1024;
+constexpr int kExpPerThread = kMaxExperts / kRouteThreads;  // 1
 
-// One workgroup of 256 threads builds the routing tables of T tokens:
-//  1. ids/weights: top-k + sigmoid of the logits (one wave per token), or the
-//     caller's ids/weights;
+// One workgroup of 1024 threads builds the routing tables of T tokens:
+//  1. ids/weights: top-k + sigmoid of the logits (one wave per token, 16
+//     tokens at a time), or the caller's ids/weights;
 //  2. each (token, expert) pair is counted once per expert (an expert listed
 //     twice for one token forms one pair whose weight is the sum), and one
 //     scan over the experts gives each routed expert its slot (ascending
@@ -1344,7 +1344,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
     __syncthreads();
     // Per entry: is it the first listing of its expert in its token, and the
     // summed weight of all listings (branch-free over the token's entries).
-    constexpr int kEntries = kMaxTokens * kMaxTopk / kRouteThreads;  // 4
+    constexpr int kEntries = kMaxTokens * kMaxTopk / kRouteThreads;  // 1
     bool take[kEntries];
     float wsum[kEntries];
 #pragma unroll
@@ -1373,9 +1373,10 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
         }
     }
     __syncthreads();
-    // Thread tid owns experts 4*tid .. 4*tid+3. Scan of (routed flag << 16 |
-    // count) (both fields stay < 2^16): serial over the thread's experts, a
-    // shuffle scan inside each wave, then wave totals in wave order.
+    // Thread tid owns experts kExpPerThread*tid .. +kExpPerThread-1. Scan of
+    // (routed flag << 16 | count) (both fields stay < 2^16): serial over the
+    // thread's experts, a shuffle scan inside each wave, then wave totals in
+    // wave order.
     int c[kExpPerThread];
     int local = 0;
 #pragma unroll
