@@ -44,7 +44,8 @@ E, K, H, O, TOPK = 256, 4096, 2048, 4096, 8
 EXPERT_BYTES = 3 * (H * K // 2 + H * K // 32)          # 13,369,344 B (W1 + W3 + W2, packed + scales)
 STAGE_A_EXPERT_BYTES = 2 * (H * K // 2 + H * K // 32)  # 8,912,896 B (W1 + W3)
 STAGE_B_EXPERT_BYTES = O * H // 2 + O * H // 32         # 4,456,448 B (W2)
-STAGE_A_KERNEL = "moe_swiglu_t1_kernel"                  # stage A's kernel at T=1
+STAGE_A_KERNEL = {1: "moe_swiglu_t1_kernel"}            # stage A's kernel by T (default: the multi-token kernel)
+STAGE_A_KERNEL_MULTI = "moe_swiglu_tn_kernel"
 
 
 def log(msg: str) -> None:
@@ -56,10 +57,11 @@ def topk_ids(logits: np.ndarray) -> np.ndarray:
 
 
 def profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` as measured by rocprofv3 counter passes
-    (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for a plain copy of
-    known size). The summaries live in profiles/*.md as lines
-    `TRAFFIC <kernel> <bytes>`; returns (bytes, file) or (None, None)."""
+    """HBM bytes per launch of `kernel` (a kernel name and the token count it
+    was measured at, e.g. "moe_swiglu_t1_kernel@T1") as measured by rocprofv3
+    counter passes (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for
+    a plain copy of known size). The summaries live in profiles/*.md as lines
+    `TRAFFIC <kernel>@T<tokens> <bytes>`; returns (bytes, file) or (None, None)."""
     d = os.path.join(REPO, "profiles")
     if not os.path.isdir(d):
         return None, None
@@ -494,9 +496,9 @@ def main() -> int:
         log("per-kernel lines: dense MXFP4, FP8, RMSNorm")
         kernels = dense_kernels(torch, dev, cpu=not args.no_cpu_baseline)
 
-    # The committed counter passes cover the one-token kernel only.
-    traffic, traffic_src = profiled_traffic(STAGE_A_KERNEL) if T == 1 else (None, None)
-    a_kernel = STAGE_A_KERNEL if T == 1 else "moe_swiglu_kernel"
+    # Counter passes are committed for T=1 and T=16; other T report null.
+    a_kernel = STAGE_A_KERNEL.get(T, STAGE_A_KERNEL_MULTI)
+    traffic, traffic_src = profiled_traffic(f"{a_kernel}@T{T}")
     result = {
         "metric": METRIC,
         "value": round(value, 2),
