@@ -164,6 +164,52 @@ def dense_kernels(torch, dev, cpu: bool) -> dict:
             out[f"fp8_e4m3_gemv {N}x{K} T={T}"] = entry(us, wbytes + T * (2 * K + 2 * N),
                                                          cpu_us(lambda: mx.fp8_gemv(xh, w, ws)))
         del W, WS
+    # Extensions on the same FP8 path: the grouped output projection wo_a
+    # (8 groups of 1024 x 4096 in one launch, against 8 single launches) and
+    # the shared expert's gate + up + SwiGLU (2048 x 4096 twice in one launch,
+    # against the two single GEMVs alone).
+    G, N, K = 8, 1024, 4096
+    w, ws = synth.fp8_weight(1100, G * N, K)
+    wbytes = G * N * K + ws.size
+    W, nW = copies(u8(w), wbytes)
+    WS = rep(u8(ws), nW)
+    xh = synth.normal_bf16(1101, (G, K))
+    xd = bf(xh)
+    y = torch.empty(G, N, dtype=torch.bfloat16, device=dev)
+    us = time_launches(lambda i: fp8b.fp8_e4m3_gemv_grouped(W[i], WS[i], xd, G, out=y), nW)
+    out["fp8_e4m3_gemv_grouped wo_a 8x1024x4096 T=1"] = entry(
+        us, wbytes + 2 * G * K + 2 * G * N, cpu_us(lambda: mx.fp8_gemv_grouped(xh, w, ws, G)))
+
+    def per_group(i):
+        for g in range(G):
+            fp8b.fp8_e4m3_gemv(W[i][g * N:(g + 1) * N], WS[i][g * N // 128:(g + 1) * N // 128], xd[g], out=y[g])
+
+    us = time_launches(per_group, nW)
+    out["fp8_e4m3_gemv_m1 x 8 wo_a (reference call pattern)"] = entry(us, wbytes + 2 * G * K + 2 * G * N, None)
+    del W, WS
+    N, K = 2048, 4096
+    w1, s1 = synth.fp8_weight(1102, N, K)
+    w3, s3 = synth.fp8_weight(1103, N, K)
+    wbytes = N * K + s1.size
+    W1, nW = copies(u8(w1), 2 * wbytes)
+    S1 = rep(u8(s1), nW)
+    W3, S3 = rep(u8(w3), nW), rep(u8(s3), nW)
+    xh = synth.normal_bf16(1104, (K,))
+    xd = bf(xh)
+    y = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    y3 = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    us = time_launches(lambda i: fp8b.fp8_e4m3_swiglu_gemv(W1[i], S1[i], W3[i], S3[i], xd, 10.0, True, out=y), nW)
+    out["fp8_e4m3_swiglu_gemv shared expert 2x2048x4096 T=1"] = entry(
+        us, 2 * wbytes + 2 * K + 2 * N, cpu_us(lambda: mx.fp8_swiglu(xh, w1, s1, w3, s3, 10.0, True)))
+
+    def two_gemvs(i):
+        fp8b.fp8_e4m3_gemv(W1[i], S1[i], xd, out=y)
+        fp8b.fp8_e4m3_gemv(W3[i], S3[i], xd, out=y3)
+
+    us = time_launches(two_gemvs, nW)
+    out["fp8_e4m3_gemv_m1 x 2 gate+up alone (reference call pattern, before its SwiGLU launch)"] = entry(
+        us, 2 * wbytes + 2 * K + 4 * N, None)
+    del W1, S1, W3, S3
     # RMSNorm + residual, H = 4096
     H = 4096
     g = synth.normal_bf16(1203, (H,), 1.0, 0.1)

@@ -38,7 +38,24 @@ struct Fp8Args {
     int64_t srow;
     uint16_t* y;
     int64_t ystride;            // elements between token rows of y
+    // Groups (blockIdx.y): group g reads x + g*xgroup, weight rows
+    // g*N .. g*N+N-1 (their scale rows (g*N+n)/128) and writes y + g*ygroup.
+    int64_t xgroup;
+    int64_t ygroup;
 };
+
+// A workgroup's view of its group: activation and output moved to the group,
+// weight row index offset by g*N (the scale row follows the global row).
+struct GroupView {
+    const uint16_t* x;
+    uint16_t* y;
+    int64_t row0;
+};
+
+__device__ __forceinline__ GroupView group_view(const Fp8Args& a) {
+    const int g = blockIdx.y;
+    return GroupView{a.x + (int64_t)g * a.xgroup, a.y + (int64_t)g * a.ygroup, (int64_t)g * a.N};
+}
 
 template <bool ALIGNED>
 __device__ __forceinline__ u32x4 load_w16(const uint8_t* p) {
@@ -57,6 +74,7 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
     const int n0 = (blockIdx.x * kWaves + wave) * kRows;
     if (n0 >= a.N) return;
     const int nseg = (a.K + NC * 1024 - 1) / (NC * 1024);
+    const GroupView gv = group_view(a);
 
     u32x4 wv[kRows][NC];
     float sc[kRows][NC];
@@ -68,8 +86,9 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
             for (int j = 0; j < NC; ++j) {
                 const int k = (seg * NC + j) * 1024 + 16 * lane;
                 if (n < a.N && k < a.K) {
-                    wv[r][j] = load_w16<ALIGNED>(a.w + (int64_t)n * a.wrow + k);
-                    sc[r][j] = e8m0_to_f32(a.s[(int64_t)(n / kTile) * a.srow + k / kTile]);
+                    const int64_t gn = gv.row0 + n;
+                    wv[r][j] = load_w16<ALIGNED>(a.w + gn * a.wrow + k);
+                    sc[r][j] = e8m0_to_f32(a.s[(gn / kTile) * a.srow + k / kTile]);
                 } else {
                     wv[r][j] = u32x4{0u, 0u, 0u, 0u};
                     sc[r][j] = 0.f;
@@ -104,7 +123,7 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
     };
     if (nseg == 1) load_rows(0);
     for (int t = 0; t < a.T; ++t) {
-        const uint16_t* xt = a.x + (int64_t)t * a.xstride;
+        const uint16_t* xt = gv.x + (int64_t)t * a.xstride;
         float acc[kRows];
 #pragma unroll
         for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
@@ -119,8 +138,23 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
         wave_reduce_n<kRows>(acc, lane);
         const int r = reduced_index<kRows>(lane);
         if (reduced_owner<kRows>(lane) && n0 + r < a.N)
-            a.y[(int64_t)t * a.ystride + n0 + r] = f32_to_bf16_bits(acc[0]);
+            gv.y[(int64_t)t * a.ystride + n0 + r] = f32_to_bf16_bits(acc[0]);
     }
+}
+
+// The second matrix and the epilogue of the fused SwiGLU launch
+// (fp8_e4m3_swiglu_gemv): y = bf16( silu(c(g)) * c_up(u) ), g and u the two
+// GEMV outputs rounded to bf16, c a clamp to [-limit, limit] (none for
+// limit <= 0), c_up the same clamp when clamp_up is set, else identity.
+struct SwigluArgs {
+    const uint8_t* w3;
+    const uint8_t* s3;
+    float limit;
+    int clamp_up;
+};
+
+__device__ __forceinline__ float swiglu_clamp(float v, float limit) {
+    return limit > 0.f ? fminf(fmaxf(v, -limit), limit) : v;
 }
 
 // Tile kernel for K in {2048, 4096} with 16-byte aligned rows and
@@ -129,62 +163,85 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
 // t, t+256, ..., t+256*(C-1) of the workgroup's [R, KC] chunk grid, so all of
 // its chunks share one k-slice (k = 16*(t % KC)) and every wave instruction
 // reads 1 KiB of a single row. Each thread issues its activation slice for all
-// TT tokens first (16 bf16 per token), then its C weight chunks and their
-// tile-scale bytes, all unconditional (rows clamped, tokens past T clamped to
-// T-1 and not stored), so everything is in flight after one issue pass.
-// Per-wave partials (C x TT values, one butterfly) meet in LDS and are added
-// in a fixed order: deterministic.
-template <int C, int TT, int KC>
-__global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a) {
+// TT tokens first (16 bf16 per token), then its C weight chunks (of each of
+// the MAT matrices) and their tile-scale bytes, all unconditional (rows
+// clamped, tokens past T clamped to T-1 and not stored), so everything is in
+// flight after one issue pass. Per-wave partials (C x TT values per matrix,
+// one butterfly per matrix) meet in LDS and are added in a fixed order:
+// deterministic, and with MAT = 2 each matrix's sums are the bits the
+// single-matrix kernel produces. blockIdx.y is the group (GroupView).
+template <int C, int TT, int KC, int MAT>
+__global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a, const SwigluArgs sw) {
     constexpr int kRowsWG = C * 256 / KC;
     constexpr int kVals = C * TT;
-    __shared__ float part[kWaves][C][TT];
+    __shared__ float part[kWaves][MAT][C][TT];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
     const int n0 = blockIdx.x * kRowsWG;
     const int k = 16 * (t % KC);
+    const GroupView gv = group_view(a);
 
     uint32_t xp[TT][8];
 #pragma unroll
     for (int tok = 0; tok < TT; ++tok) {
-        const u32x4* s4 = reinterpret_cast<const u32x4*>(a.x + (int64_t)min(tok, a.T - 1) * a.xstride + k);
+        const u32x4* s4 = reinterpret_cast<const u32x4*>(gv.x + (int64_t)min(tok, a.T - 1) * a.xstride + k);
         const u32x4 v0 = s4[0], v1 = s4[1];
         xp[tok][0] = v0[0]; xp[tok][1] = v0[1]; xp[tok][2] = v0[2]; xp[tok][3] = v0[3];
         xp[tok][4] = v1[0]; xp[tok][5] = v1[1]; xp[tok][6] = v1[2]; xp[tok][7] = v1[3];
     }
     __builtin_amdgcn_sched_barrier(0);  // activation loads first
-    u32x4 w[C];
-    uint32_t sb[C];
+    u32x4 w[MAT][C];
+    uint32_t sb[MAT][C];
 #pragma unroll
     for (int i = 0; i < C; ++i) {
-        const int n = min(n0 + (t + 256 * i) / KC, a.N - 1);
-        w[i] = ld16_stream(a.w + (int64_t)n * a.wrow + k);
-        sb[i] = a.s[(int64_t)(n / kTile) * a.srow + k / kTile];
+        const int64_t gn = gv.row0 + min(n0 + (t + 256 * i) / KC, a.N - 1);
+        w[0][i] = ld16_stream(a.w + gn * a.wrow + k);
+        sb[0][i] = a.s[(gn / kTile) * a.srow + k / kTile];
+        if constexpr (MAT == 2) {
+            w[1][i] = ld16_stream(sw.w3 + gn * a.wrow + k);
+            sb[1][i] = sw.s3[(gn / kTile) * a.srow + k / kTile];
+        }
     }
-    float acc[kVals];
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-        const float sc = e8m0_to_f32(sb[i]);
+    for (int m = 0; m < MAT; ++m) {
+        float acc[kVals];
 #pragma unroll
-        for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[i], xp[tok]) * sc;
+        for (int i = 0; i < C; ++i) {
+            const float sc = e8m0_to_f32(sb[m][i]);
+#pragma unroll
+            for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[m][i], xp[tok]) * sc;
+        }
+        wave_reduce_n<kVals>(acc, lane);
+        const int v = reduced_index<kVals>(lane);
+        if (reduced_owner<kVals>(lane)) part[wave][m][v / TT][v % TT] = acc[0];
     }
-    wave_reduce_n<kVals>(acc, lane);
-    const int v = reduced_index<kVals>(lane);
-    if (reduced_owner<kVals>(lane)) part[wave][v / TT][v % TT] = acc[0];
     __syncthreads();
     for (int o = t; o < kRowsWG * TT; o += 256) {
         const int r = o / TT;
         const int tok = o % TT;
         if (tok >= a.T || n0 + r >= a.N) continue;
-        float sum = 0.f;
+        float sum[MAT];
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
+        for (int m = 0; m < MAT; ++m) {
+            sum[m] = 0.f;
 #pragma unroll
-            for (int i = 0; i < C; ++i)
-                if ((64 * w2 + 256 * i) / KC == r) sum += part[w2][i][tok];
+            for (int w2 = 0; w2 < kWaves; ++w2) {
+#pragma unroll
+                for (int i = 0; i < C; ++i)
+                    if ((64 * w2 + 256 * i) / KC == r) sum[m] += part[w2][m][i][tok];
+            }
         }
-        a.y[(int64_t)tok * a.ystride + n0 + r] = f32_to_bf16_bits(sum);
+        uint16_t out;
+        if constexpr (MAT == 2) {
+            const float g = swiglu_clamp(bf16_bits_to_f32(f32_to_bf16_bits(sum[0])), sw.limit);
+            const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(sum[1]));
+            const float u = sw.clamp_up ? swiglu_clamp(u0, sw.limit) : u0;
+            out = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+        } else {
+            out = f32_to_bf16_bits(sum[0]);
+        }
+        gv.y[(int64_t)tok * a.ystride + n0 + r] = out;
     }
 }
 
@@ -229,44 +286,53 @@ int validate(int K, int N) {
     return 0;
 }
 
-int launch(const Fp8Args& a, hipStream_t stream) {
-    const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) &&
-                    (a.T == 1 || a.xstride % 8 == 0);
-    if (al && (a.K == 2048 || a.K == 4096)) {
-        // Four chunks per thread: 4 rows per workgroup at K = 4096, 8 at 2048.
-        const int KC = a.K / 16;
-        const int rows = 4 * 256 / KC;
-        const dim3 grid((unsigned)((a.N + rows - 1) / rows));
-#define DSV4_TILE(TTV)                                                                            \
-    if (KC == 256) hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 256>), grid, dim3(256), 0, stream, a); \
-    else hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 128>), grid, dim3(256), 0, stream, a);
-        if (a.T == 1) { DSV4_TILE(1) }
-        else if (a.T == 2) { DSV4_TILE(2) }
-        else if (a.T <= 4) { DSV4_TILE(4) }
-        else if (a.T <= 8) { DSV4_TILE(8) }
-        else { DSV4_TILE(16) }
+bool tile_ok(const Fp8Args& a) {
+    return aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) && (a.T == 1 || a.xstride % 8 == 0) &&
+           (a.xgroup % 8 == 0) && (a.K == 2048 || a.K == 4096);
+}
+
+// G groups (grid.y). MAT = 2: the fused SwiGLU (tile shapes only, T <= 8
+// per launch).
+template <int MAT>
+hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
+    // Four chunks per thread: 4 rows per workgroup at K = 4096, 8 at 2048.
+    const int KC = a.K / 16;
+    const int rows = 4 * 256 / KC;
+    const dim3 grid((unsigned)((a.N + rows - 1) / rows), (unsigned)G);
+#define DSV4_TILE(TTV)                                                                                          \
+    if (KC == 256) hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 256, MAT>), grid, dim3(256), 0, stream, a, sw); \
+    else hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 128, MAT>), grid, dim3(256), 0, stream, a, sw);
+    if (a.T == 1) { DSV4_TILE(1) }
+    else if (a.T == 2) { DSV4_TILE(2) }
+    else if (a.T <= 4) { DSV4_TILE(4) }
+    else if (a.T <= 8 || MAT == 2) { DSV4_TILE(8) }
+    else { DSV4_TILE(16) }
 #undef DSV4_TILE
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) {
-            std::fprintf(stderr, "fp8_e4m3_gemv launch failed: %s\n", hipGetErrorString(e));
-            return -4;
-        }
-        return 0;
-    }
-    const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)));
-    const dim3 block(64 * kWaves);
-    const int nc = (a.K + 1023) / 1024;
+    return hipGetLastError();
+}
+
+int launch(const Fp8Args& a, int G, hipStream_t stream) {
+    hipError_t e;
+    if (tile_ok(a)) {
+        e = launch_tile<1>(a, SwigluArgs{}, G, stream);
+    } else {
+        const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);
+        const dim3 block(64 * kWaves);
+        const int nc = (a.K + 1023) / 1024;
+        const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) &&
+                        (a.T == 1 || a.xstride % 8 == 0) && (a.xgroup % 8 == 0);
 #define DSV4_LAUNCH(NCV)                                                                    \
     if (al) hipLaunchKernelGGL((fp8_gemv_kernel<NCV, true>), grid, block, 0, stream, a);   \
     else hipLaunchKernelGGL((fp8_gemv_kernel<NCV, false>), grid, block, 0, stream, a);
-    switch (nc) {
-        case 1: DSV4_LAUNCH(1) break;
-        case 2: DSV4_LAUNCH(2) break;
-        case 3: DSV4_LAUNCH(3) break;
-        default: DSV4_LAUNCH(4) break;
-    }
+        switch (nc) {
+            case 1: DSV4_LAUNCH(1) break;
+            case 2: DSV4_LAUNCH(2) break;
+            case 3: DSV4_LAUNCH(3) break;
+            default: DSV4_LAUNCH(4) break;
+        }
 #undef DSV4_LAUNCH
-    const hipError_t e = hipGetLastError();
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) {
         std::fprintf(stderr, "fp8_e4m3_gemv launch failed: %s\n", hipGetErrorString(e));
         return -4;
@@ -282,8 +348,8 @@ extern "C" int fp8_e4m3_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_fp8, cons
     const int v = validate(K, N);
     if (v != 0) return v;
     Fp8Args a{reinterpret_cast<const uint16_t*>(x), K, W_fp8, W_scale, K, N, 1,
-              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y), N};
-    return launch(a, stream);
+              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y), N, 0, 0};
+    return launch(a, 1, stream);
 }
 
 extern "C" int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
@@ -298,8 +364,64 @@ extern "C" int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const u
     }
     Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W_fp8, W_scale, K, N, T,
               weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y),
-              y_row_stride};
-    return launch(a, stream);
+              y_row_stride, 0, 0};
+    return launch(a, 1, stream);
+}
+
+extern "C" int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_group_stride,
+                                     const uint8_t* W_fp8, const uint8_t* W_scale, int G, int K, int N,
+                                     int T, int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                                     dsv4_bf16_t* y, int64_t y_row_stride, int64_t y_group_stride,
+                                     hipStream_t stream) {
+    const int v = validate(K, N);
+    if (v != 0) return v;
+    if (T < 1 || T > kMaxT) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_grouped: T=%d outside [1, %d]\n", T, kMaxT);
+        return -5;
+    }
+    if (G < 1 || G > 65535) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_grouped: G=%d outside [1, 65535]\n", G);
+        return -6;
+    }
+    Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W_fp8, W_scale, K, N, T,
+              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y),
+              y_row_stride, x_group_stride, y_group_stride};
+    return launch(a, G, stream);
+}
+
+extern "C" int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W1_fp8,
+                                    const uint8_t* W1_scale, const uint8_t* W3_fp8, const uint8_t* W3_scale,
+                                    int K, int N, int T, int64_t weight_row_stride_bytes,
+                                    int64_t scale_row_stride_bytes, float limit, int clamp_up,
+                                    dsv4_bf16_t* act, int64_t act_row_stride, hipStream_t stream) {
+    const int v = validate(K, N);
+    if (v != 0) return v;
+    if (T < 1 || T > kMaxT) {
+        std::fprintf(stderr, "fp8_e4m3_swiglu_gemv: T=%d outside [1, %d]\n", T, kMaxT);
+        return -5;
+    }
+    Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W1_fp8, W1_scale, K, N, T,
+              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(act),
+              act_row_stride, 0, 0};
+    if (!tile_ok(a) || !aligned16(W3_fp8)) {
+        std::fprintf(stderr, "fp8_e4m3_swiglu_gemv: needs K in {2048, 4096} and 16-byte aligned x, W1, W3 "
+                             "and rows\n");
+        return -6;
+    }
+    const SwigluArgs sw{W3_fp8, W3_scale, limit, clamp_up};
+    // At most 8 tokens per launch (registers of the two matrices' partials).
+    for (int t0 = 0; t0 < T; t0 += 8) {
+        Fp8Args c = a;
+        c.x = a.x + (int64_t)t0 * x_row_stride;
+        c.y = a.y + (int64_t)t0 * act_row_stride;
+        c.T = T - t0 < 8 ? T - t0 : 8;
+        const hipError_t e = launch_tile<2>(c, sw, 1, stream);
+        if (e != hipSuccess) {
+            std::fprintf(stderr, "fp8_e4m3_swiglu_gemv launch failed: %s\n", hipGetErrorString(e));
+            return -4;
+        }
+    }
+    return 0;
 }
 
 extern "C" int fp8_e4m3_dequant_bf16(const uint8_t* W_fp8, const uint8_t* W_scale, int K, int N,

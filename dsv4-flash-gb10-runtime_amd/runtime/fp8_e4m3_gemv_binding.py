@@ -45,6 +45,10 @@ def _load_lib() -> ctypes.CDLL:
         lib.fp8_e4m3_gemv.restype = I
         lib.fp8_e4m3_dequant_bf16.argtypes = [P, P, I, I, L, L, P, P]
         lib.fp8_e4m3_dequant_bf16.restype = I
+        lib.fp8_e4m3_gemv_grouped.argtypes = [P, L, L, P, P, I, I, I, I, L, L, P, L, L, P]
+        lib.fp8_e4m3_gemv_grouped.restype = I
+        lib.fp8_e4m3_swiglu_gemv.argtypes = [P, L, P, P, P, P, I, I, I, L, L, ctypes.c_float, I, P, L, P]
+        lib.fp8_e4m3_swiglu_gemv.restype = I
         _LIB = lib
     return _LIB
 
@@ -111,6 +115,93 @@ def fp8_e4m3_gemv(
         name = "fp8_e4m3_gemv"
     if rc != 0:
         raise RuntimeError(f"{name} returned {rc}")
+    return out
+
+
+def fp8_e4m3_gemv_grouped(
+    W_fp8: torch.Tensor,
+    W_scale: torch.Tensor,
+    x: torch.Tensor,
+    groups: int,
+    out: Optional[torch.Tensor] = None,
+    stream: Optional[torch.cuda.Stream] = None,
+) -> torch.Tensor:
+    """G GEMVs in one launch: W [G*N, K] holds the groups' weights stacked by
+    rows; x [G, K] or [T, G, K]; y[..., g, :] = x[..., g, :] @ dequant(W[g*N:(g+1)*N]).T
+    ([G, N] or [T, G, N]). The grouped output projection wo_a (G=8, N=1024,
+    K=4096) of kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:484-499."""
+    _check_w(W_fp8, W_scale)
+    if not x.is_cuda or x.dtype != torch.bfloat16:
+        raise RuntimeError("x must be a GPU bfloat16 tensor")
+    if x.dim() not in (2, 3):
+        raise RuntimeError(f"x must be [G, K] or [T, G, K], got shape {tuple(x.shape)}")
+    GN, K = W_fp8.shape
+    G = groups
+    if G < 1 or GN % G != 0:
+        raise RuntimeError(f"W rows {GN} are not a multiple of groups={G}")
+    N = GN // G
+    if x.shape[-2:] != (G, K):
+        raise RuntimeError(f"x trailing shape {tuple(x.shape[-2:])} != ({G}, {K})")
+    T = 1 if x.dim() == 2 else x.shape[0]
+    if T > MAX_TOKENS:
+        raise RuntimeError(f"T={T} > {MAX_TOKENS}")
+    x = x.contiguous()
+    oshape = (G, N) if x.dim() == 2 else (T, G, N)
+    if out is None:
+        out = torch.empty(oshape, dtype=torch.bfloat16, device=x.device)
+    elif tuple(out.shape) != oshape or out.dtype != torch.bfloat16 or not out.is_cuda \
+            or not out.is_contiguous():
+        raise RuntimeError(f"out must be a contiguous GPU bfloat16 {oshape} tensor")
+    rc = _load_lib().fp8_e4m3_gemv_grouped(
+        _lib.vp(x), G * K, K, _lib.vp(W_fp8), _lib.vp(W_scale), G, K, N, T, W_fp8.stride(0),
+        W_scale.stride(0), _lib.vp(out), G * N, N, ctypes.c_void_p(_lib.stream_ptr(x.device, stream)))
+    if rc != 0:
+        raise RuntimeError(f"fp8_e4m3_gemv_grouped returned {rc}")
+    return out
+
+
+def fp8_e4m3_swiglu_gemv(
+    W1_fp8: torch.Tensor,
+    W1_scale: torch.Tensor,
+    W3_fp8: torch.Tensor,
+    W3_scale: torch.Tensor,
+    x: torch.Tensor,
+    limit: float = 10.0,
+    clamp_up: bool = True,
+    out: Optional[torch.Tensor] = None,
+    stream: Optional[torch.cuda.Stream] = None,
+) -> torch.Tensor:
+    """act = bf16( silu(clamp(bf16(W1 x))) * clamp?(bf16(W3 x)) ) in one launch:
+    the shared expert's gate, up and SwiGLU (runtime/dsv4_engine_mxfp4.py:399-410,
+    which clamps both, clamp_up=True; kernel/cpp-engine-mxfp4/
+    dsv4_engine_mxfp4_wire.cu:510-548 clamps the gate only, clamp_up=False).
+    x [K] or [T, K]; K must be 2048 or 4096."""
+    _check_w(W1_fp8, W1_scale)
+    _check_w(W3_fp8, W3_scale)
+    if W1_fp8.shape != W3_fp8.shape or W1_fp8.stride() != W3_fp8.stride() \
+            or W1_scale.stride() != W3_scale.stride():
+        raise RuntimeError("W1 and W3 must have the same shape and strides")
+    if not x.is_cuda or x.dtype != torch.bfloat16 or x.dim() not in (1, 2):
+        raise RuntimeError("x must be a GPU bfloat16 [K] or [T, K] tensor")
+    N, K = W1_fp8.shape
+    if x.shape[-1] != K:
+        raise RuntimeError(f"x last dim {x.shape[-1]} != K={K}")
+    T = 1 if x.dim() == 1 else x.shape[0]
+    if T > MAX_TOKENS:
+        raise RuntimeError(f"T={T} > {MAX_TOKENS}")
+    x = x.contiguous()
+    oshape = (N,) if x.dim() == 1 else (T, N)
+    if out is None:
+        out = torch.empty(oshape, dtype=torch.bfloat16, device=x.device)
+    elif tuple(out.shape) != oshape or out.dtype != torch.bfloat16 or not out.is_cuda \
+            or not out.is_contiguous():
+        raise RuntimeError(f"out must be a contiguous GPU bfloat16 {oshape} tensor")
+    rc = _load_lib().fp8_e4m3_swiglu_gemv(
+        _lib.vp(x), K, _lib.vp(W1_fp8), _lib.vp(W1_scale), _lib.vp(W3_fp8), _lib.vp(W3_scale), K, N, T,
+        W1_fp8.stride(0), W1_scale.stride(0), float(limit), int(bool(clamp_up)), _lib.vp(out), N,
+        ctypes.c_void_p(_lib.stream_ptr(x.device, stream)))
+    if rc != 0:
+        raise RuntimeError(f"fp8_e4m3_swiglu_gemv returned {rc}")
     return out
 
 

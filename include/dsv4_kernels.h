@@ -11,8 +11,9 @@
  *   kernel/mxfp4-dense/libmxfp4_gemv.so           mxfp4_gemv_m1,
  *                                                 mxfp4_dequant_bf16 (extension)
  *   kernel/fp8-dense/libfp8_e4m3_gemv.so          fp8_e4m3_gemv_m1,
- *                                                 fp8_e4m3_gemv, fp8_e4m3_dequant_bf16
- *                                                 (extensions)
+ *                                                 fp8_e4m3_gemv, fp8_e4m3_gemv_grouped,
+ *                                                 fp8_e4m3_swiglu_gemv,
+ *                                                 fp8_e4m3_dequant_bf16 (extensions)
  *   kernel/rmsnorm-fuse/librmsnorm_fuse.so        rmsnorm_fuse_fwd,
  *                                                 rmsnorm_fuse_residual_add
  *
@@ -201,6 +202,38 @@ int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_f
                   const uint8_t* W_scale, int K, int N, int T,
                   int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
                   dsv4_bf16_t* y, int64_t y_row_stride, hipStream_t stream);
+
+/* EXTENSION (replaces the per-group loop of 8 fp8_e4m3_gemv_m1 calls for the
+ * grouped output projection wo_a, reference
+ * kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:484-499, and the einsum
+ * of runtime/dsv4_engine_mxfp4.py:515-528): G GEMVs in one launch.
+ *   y[t, g, n] = bf16( sum_k W[g*N + n, k] x[t, g, k] ),  g < G, n < N, t < T
+ * with W [G*N, K] (scale rows (g*N+n)/128), x element (t, g, k) at
+ * x + t*x_row_stride + g*x_group_stride + k, y element (t, g, n) at
+ * y + t*y_row_stride + g*y_group_stride + n. Returns as fp8_e4m3_gemv, plus
+ * -6 for G < 1 or G > 65535. */
+int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_group_stride,
+                          const uint8_t* W_fp8, const uint8_t* W_scale, int G, int K, int N, int T,
+                          int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                          dsv4_bf16_t* y, int64_t y_row_stride, int64_t y_group_stride,
+                          hipStream_t stream);
+
+/* EXTENSION (replaces the gate GEMV, the up GEMV and the SwiGLU launch of the
+ * shared expert, reference kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:
+ * 508-548 and runtime/dsv4_engine_mxfp4.py:399-410): one launch for
+ *   act[t, n] = bf16( silu(c(g)) * c_up(u) ),  silu(v) = v / (1 + expf(-v)),
+ * g = bf16(W1 x_t)[n] and u = bf16(W3 x_t)[n] (each exactly the bits
+ * fp8_e4m3_gemv writes), c a clamp to [-limit, limit] (no clamp for
+ * limit <= 0), c_up the same clamp if clamp_up != 0 (runtime/dsv4_engine_mxfp4.py:
+ * 405-407 clamps both) else none (dsv4_engine_mxfp4_wire.cu:517-518 clamps the
+ * gate only). W1, W3 share K, N and row strides. Needs K in {2048, 4096} and
+ * 16-byte aligned x, W1, W3 and rows (-6 otherwise); T in [1, 16] (-5).
+ * Returns as fp8_e4m3_gemv otherwise. */
+int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W1_fp8,
+                         const uint8_t* W1_scale, const uint8_t* W3_fp8, const uint8_t* W3_scale,
+                         int K, int N, int T, int64_t weight_row_stride_bytes,
+                         int64_t scale_row_stride_bytes, float limit, int clamp_up,
+                         dsv4_bf16_t* act, int64_t act_row_stride, hipStream_t stream);
 
 /* EXTENSION (debug): out[n,k] = bf16( e4m3(W[n,k]) * 2^(S[n/128,k/128]-127) ),
  * the device decode of the FP8 GEMVs, for the bit-exact check against

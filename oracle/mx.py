@@ -177,6 +177,45 @@ def fp8_gemv(x, w, s) -> np.ndarray:
     return bf16_round(_matvec_f32(fp8_dequant_bf16(w, s), x))
 
 
+def fp8_gemv_grouped(x, w, s, groups: int) -> np.ndarray:
+    """G GEMVs over row groups of one FP8 matrix: w [G*N, K], x [G, K] or
+    [T, G, K] bf16 bits -> y[..., g, n] = bf16( x[..., g, :] . dequant(w)[g*N + n] ),
+    the scale row following the global row (g*N + n) / 128
+    (kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:484-499: the wo_a
+    slices W_g = wo_a + g*1024 rows, S_g = + g*8 scale rows)."""
+    W = bf16_to_f32(fp8_dequant_bf16(w, s))
+    GN, K = W.shape
+    N = GN // groups
+    xf = bf16_to_f32(np.asarray(x, dtype=np.uint16))
+    Wg = W.reshape(groups, N, K)
+    y = np.einsum("...gk,gnk->...gn", xf.astype(np.float64), Wg.astype(np.float64))
+    return bf16_round(y.astype(np.float32))
+
+
+def swiglu_clamped(gate_bits, up_bits, limit: float, clamp_up: bool) -> np.ndarray:
+    """act = bf16( silu(c(g)) * c_up(u) ) on bf16 gate/up, fp32 math, one
+    rounding: the shared expert's SwiGLU (kernel/cpp-engine-mxfp4/
+    dsv4_engine_mxfp4_wire.cu:510-521 clamps the gate only, clamp_up=False;
+    runtime/dsv4_engine_mxfp4.py:405-408 clamps both, clamp_up=True, and rounds
+    silu and the product to bf16 separately, a difference within tolerance).
+    c clamps to [-limit, limit]; limit <= 0 disables both clamps."""
+    g = bf16_to_f32(gate_bits).astype(np.float32)
+    u = bf16_to_f32(up_bits).astype(np.float32)
+    if limit > 0:
+        g = np.clip(g, -limit, limit).astype(np.float32)
+        if clamp_up:
+            u = np.clip(u, -limit, limit).astype(np.float32)
+    with np.errstate(over="ignore"):
+        sil = (g / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
+    return bf16_round((sil * u).astype(np.float32))
+
+
+def fp8_swiglu(x, w1, s1, w3, s3, limit: float, clamp_up: bool) -> np.ndarray:
+    """The shared expert's gate, up and SwiGLU: swiglu_clamped(fp8_gemv(W1),
+    fp8_gemv(W3)) (dsv4_engine_mxfp4_wire.cu:528-548)."""
+    return swiglu_clamped(fp8_gemv(x, w1, s1), fp8_gemv(x, w3, s3), limit, clamp_up)
+
+
 def silu_f32(v) -> np.ndarray:
     """x / (1 + exp(-x)) in fp32 (kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:122-124)."""
     v = np.asarray(v, dtype=np.float32)

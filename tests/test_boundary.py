@@ -22,7 +22,8 @@ LIBS = {
         "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer",
         "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
-    "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_dequant_bf16"],
+    "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
+                                      "fp8_e4m3_swiglu_gemv", "fp8_e4m3_dequant_bf16"],
     "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],
 }
 
@@ -181,6 +182,19 @@ def test_fp8_validation_codes():
     assert g(N, 4096, N, N, 4096, 1536, 0, 4096, 32, N, 1536, N) == -5
     assert g(N, 4096, N, N, 4096, 1536, 17, 4096, 32, N, 1536, N) == -5
     assert g(N, 4096, N, N, 4000, 1536, 2, 4096, 32, N, 1536, N) == -1
+    gr = lib.fp8_e4m3_gemv_grouped
+    gr.restype = I
+    gr.argtypes = [P, L, L, P, P, I, I, I, I, L, L, P, L, L, P]
+    assert gr(N, 32768, 4096, N, N, 0, 4096, 1024, 1, 4096, 32, N, 8192, 1024, N) == -6
+    assert gr(N, 32768, 4096, N, N, 8, 4096, 1024, 17, 4096, 32, N, 8192, 1024, N) == -5
+    assert gr(N, 32768, 4096, N, N, 8, 4000, 1024, 1, 4096, 32, N, 8192, 1024, N) == -1
+    sw = lib.fp8_e4m3_swiglu_gemv
+    sw.restype = I
+    sw.argtypes = [P, L, P, P, P, P, I, I, I, L, L, ctypes.c_float, I, P, L, P]
+    assert sw(N, 4096, N, N, N, N, 4096, 2048, 0, 4096, 32, 10.0, 1, N, 2048, N) == -5
+    assert sw(N, 4096, N, N, N, N, 4000, 2048, 1, 4096, 32, 10.0, 1, N, 2048, N) == -1
+    # K = 1024 is a valid GEMV shape that the fused kernel does not take
+    assert sw(N, 1024, N, N, N, N, 1024, 2048, 1, 1024, 8, 10.0, 1, N, 2048, N) == -6
 
 
 def test_rmsnorm_validation_codes():

@@ -155,6 +155,55 @@ def test_fp8_gemv_long_rows_and_ragged_n(device):
     assert_close(host_bits(y), mx.fp8_gemv(x, w, s), "fp8 K=8192")
 
 
+@pytest.mark.parametrize("G,N,K,T", [(8, 1024, 4096, 1), (8, 1024, 4096, 3), (3, 576, 2048, 2),
+                                     (4, 64, 4096, 1), (2, 200, 1024, 2)])
+def test_fp8_gemv_grouped(device, G, N, K, T):
+    """G GEMVs in one launch (the wo_a shape G=8, N=1024, K=4096 first): against
+    the oracle, and, for 128-row groups on the tile path, bit for bit against
+    one fp8_e4m3_gemv call per group on that group's slice. N=576 and N=64
+    put group boundaries inside a scale tile; K=1024 takes the general kernel."""
+    announce(f"fp8_e4m3_gemv_grouped G={G} N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(4300 + G + N, G * N, K)
+    x = synth.normal_bf16(4400 + T, (T, G, K))
+    tw, ts = dev_u8(w, device), dev_u8(s, device)
+    xd = dev_bf16(x, device)
+    y = fp8b.fp8_e4m3_gemv_grouped(tw, ts, xd if T > 1 else xd[0], G)
+    got = host_bits(y).reshape(T, G, N)
+    assert_close(got.reshape(T, -1), mx.fp8_gemv_grouped(x, w, s, G).reshape(T, -1), f"fp8 grouped G={G}")
+    if N % 128 == 0 and K in (2048, 4096):
+        for g in range(G):
+            yg = fp8b.fp8_e4m3_gemv(tw[g * N:(g + 1) * N], ts[g * N // 128:(g + 1) * N // 128],
+                                    xd[:, g].contiguous() if T > 1 else xd[0, g].contiguous())
+            assert np.array_equal(host_bits(yg).reshape(T, N), got[:, g]), f"group {g}"
+
+
+@pytest.mark.parametrize("N,K,T,clamp_up", [(2048, 4096, 1, True), (2048, 4096, 1, False),
+                                            (2048, 4096, 5, True), (2048, 4096, 16, False),
+                                            (300, 2048, 3, True)])
+def test_fp8_swiglu_gemv(device, N, K, T, clamp_up):
+    """The shared expert's gate + up + SwiGLU in one launch (N=2048, K=4096):
+    gate and up are the bits of the two single GEMVs, the clamp at 10 is
+    exercised (activations scaled so some gate and up values pass it), and the
+    result matches the oracle."""
+    announce(f"fp8_e4m3_swiglu_gemv N={N} K={K} T={T} clamp_up={clamp_up}")
+    w1, s1 = synth.fp8_weight(4500 + N, N, K)
+    w3, s3 = synth.fp8_weight(4600 + N, N, K)
+    x = mx.bf16_round(24 * mx.bf16_to_f32(synth.normal_bf16(4700 + T, (T, K))))
+    t1, u1, t3, u3 = dev_u8(w1, device), dev_u8(s1, device), dev_u8(w3, device), dev_u8(s3, device)
+    xd = dev_bf16(x, device)
+    act = host_bits(fp8b.fp8_e4m3_swiglu_gemv(t1, u1, t3, u3, xd if T > 1 else xd[0], 10.0, clamp_up))
+    act = act.reshape(T, N)
+    gate = host_bits(fp8b.fp8_e4m3_gemv(t1, u1, xd if T > 1 else xd[0])).reshape(T, N)
+    up = host_bits(fp8b.fp8_e4m3_gemv(t3, u3, xd if T > 1 else xd[0])).reshape(T, N)
+    assert np.abs(mx.bf16_to_f32(gate)).max() > 10 and np.abs(mx.bf16_to_f32(up)).max() > 10
+    # the epilogue on the single GEMVs' bits: equal up to expf's last bit
+    ref_bits = mx.swiglu_clamped(gate, up, 10.0, clamp_up)
+    diff = np.abs(act.astype(np.int32) - ref_bits.astype(np.int32))
+    diff[mx.bf16_to_f32(act) == mx.bf16_to_f32(ref_bits)] = 0  # +0 and -0
+    assert diff.max() <= 1, f"max bf16 ulp difference {diff.max()}"
+    assert_close(act, mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, clamp_up), f"fp8 swiglu T={T}")
+
+
 # ------------------------------------------------------ grouped (drop-in) --
 
 def _packed_experts(seed, n, K, H, O):

@@ -85,6 +85,81 @@ def test_fp8_gemv_brute_force_and_c_oracle():
     assert rel < 1e-2 and cos > 0.99999
 
 
+def test_fp8_gemv_grouped_slices_and_scale_rows():
+    # 128-row groups: each group is an independent GEMV on its own slice
+    w, s = synth.fp8_weight(60, 3 * 128, 256)
+    x = synth.normal_bf16(61, (3, 256))
+    y = mx.fp8_gemv_grouped(x, w, s, 3)
+    for g in range(3):
+        ref = mx.fp8_gemv(x[g], w[128 * g:128 * (g + 1)], s[g:g + 1])
+        assert np.array_equal(y[g], ref)
+    # 64-row groups share scale rows: the scale row follows the global row
+    w, s = synth.fp8_weight(62, 4 * 64, 256)
+    x = synth.normal_bf16(63, (2, 4, 256))
+    y = mx.fp8_gemv_grouped(x, w, s, 4)
+    vals = mx.e4m3fn_decode(w).astype(np.float64)
+    sc = np.array([[2.0 ** (int(s[n // 128, k // 128]) - 127) for k in range(256)] for n in range(256)])
+    Wf = vals * sc
+    for t in range(2):
+        for g in range(4):
+            ref = mx.bf16_to_f32(x[t, g]).astype(np.float64) @ Wf[64 * g:64 * (g + 1)].T
+            rel, cos = mx.compare(y[t, g], mx.bf16_round(ref.astype(np.float32)))
+            assert rel < 1e-2 and cos > 0.99999
+    # one group is the plain GEMV
+    assert np.array_equal(mx.fp8_gemv_grouped(x[:, :1], w[:64], s[:1], 1)[:, 0], mx.fp8_gemv(x[:, 0], w[:64], s[:1]))
+
+
+def test_swiglu_clamped_closed_forms():
+    def b(v):
+        return mx.bf16_round(np.asarray(v, np.float32))
+
+    def val(bits):
+        return float(np.asarray(mx.bf16_to_f32(bits)).reshape(-1)[0])
+
+    def silu(v):
+        return v / (1.0 + np.exp(-v))
+
+    # gate 0 gives 0; no clamp inside the limit
+    assert val(mx.swiglu_clamped(b(0.0), b(3.0), 10.0, True)) == 0.0
+    assert np.isclose(val(mx.swiglu_clamped(b(2.0), b(3.0), 10.0, True)), silu(2.0) * 3.0, rtol=4e-3)
+    # the gate is clamped to +-limit
+    assert np.isclose(val(mx.swiglu_clamped(b(100.0), b(1.0), 10.0, False)), silu(10.0), rtol=4e-3)
+    assert np.isclose(val(mx.swiglu_clamped(b(-100.0), b(1.0), 10.0, False)), silu(-10.0), rtol=4e-3)
+    # up is clamped only with clamp_up
+    assert np.isclose(val(mx.swiglu_clamped(b(1.0), b(-50.0), 10.0, True)), silu(1.0) * -10.0, rtol=4e-3)
+    assert np.isclose(val(mx.swiglu_clamped(b(1.0), b(-50.0), 10.0, False)), silu(1.0) * -50.0, rtol=4e-3)
+    # limit <= 0: no clamp at all
+    assert np.isclose(val(mx.swiglu_clamped(b(100.0), b(-50.0), 0.0, True)), 100.0 * -50.0, rtol=4e-3)
+    # a random batch against fp64 with one final rounding
+    rng = np.random.default_rng(64)
+    g = b(rng.normal(0, 8, 4096))
+    u = b(rng.normal(0, 8, 4096))
+    gf = np.clip(mx.bf16_to_f32(g).astype(np.float64), -10, 10)
+    uf = np.clip(mx.bf16_to_f32(u).astype(np.float64), -10, 10)
+    rel, cos = mx.compare(mx.swiglu_clamped(g, u, 10.0, True), mx.bf16_round((silu(gf) * uf).astype(np.float32)))
+    assert rel < 1e-2 and cos > 0.99999
+
+
+def test_fp8_swiglu_brute_force():
+    w1, s1 = synth.fp8_weight(65, 130, 256)
+    w3, s3 = synth.fp8_weight(66, 130, 256)
+    x = mx.bf16_round(24 * mx.bf16_to_f32(synth.normal_bf16(67, (2, 256))))  # some gates past the limit
+    act = mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, False)
+
+    def dense(w, s):
+        vals = mx.e4m3fn_decode(w).astype(np.float64)
+        sc = np.array([[2.0 ** (int(s[n // 128, k // 128]) - 127) for k in range(256)] for n in range(130)])
+        return vals * sc
+
+    xf = mx.bf16_to_f32(x).astype(np.float64)
+    g = np.clip(xf @ dense(w1, s1).T, -10, 10)
+    u = xf @ dense(w3, s3).T
+    assert np.abs(xf @ dense(w1, s1).T).max() > 10  # the clamp is exercised
+    ref = mx.bf16_round((g / (1 + np.exp(-g)) * u).astype(np.float32))
+    rel, cos = mx.compare(act, ref)
+    assert rel < 2e-2 and cos > 0.9999
+
+
 def _experts(seed, n, K, H, O):
     W1p, W1s = synth.mxfp4_weight(seed, H, K, n)
     W3p, W3s = synth.mxfp4_weight(seed + 4, H, K, n)
