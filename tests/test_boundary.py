@@ -46,6 +46,21 @@ def _declared():
     return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(\w+)\s*\(", text, flags=re.M)))
 
 
+STORE_HEADER = os.path.join(REPO, "include", "dsv4_expert_store.h")
+STORE_LIB = "expert-store/libdsv4_expert_store.so"
+
+
+def test_expert_store_header_matches_exports():
+    text = re.sub(r"/\*.*?\*/", "", open(STORE_HEADER).read(), flags=re.S)
+    declared = sorted(set(re.findall(r"^\s*(?:int|dsv4_store\s*\*)\s*(\w+)\s*\(", text, flags=re.M)))
+    assert declared == ["dsv4_store_close", "dsv4_store_count", "dsv4_store_load_experts",
+                        "dsv4_store_load_tensor", "dsv4_store_open", "dsv4_store_read",
+                        "dsv4_store_tensor_info"]
+    lib = _lib(STORE_LIB)
+    for sym in declared:
+        assert hasattr(lib, sym), f"{STORE_LIB} does not export {sym}"
+
+
 def test_header_declares_exactly_the_exported_set():
     declared = _declared()
     exported = sorted(s for syms in LIBS.values() for s in syms)
