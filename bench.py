@@ -210,6 +210,29 @@ def dense_kernels(torch, dev, cpu: bool) -> dict:
     out["fp8_e4m3_gemv_m1 x 2 gate+up alone (reference call pattern, before its SwiGLU launch)"] = entry(
         us, 2 * wbytes + 2 * K + 4 * N, None)
     del W1, S1, W3, S3
+    # RMSNorm + residual folded into the wq_a GEMV (1536 x 4096), against the
+    # two launches (RMSNorm, then the GEMV on its output).
+    N, K = 1536, 4096
+    w, ws = synth.fp8_weight(1105, N, K)
+    wbytes = N * K + ws.size
+    W, nW = copies(u8(w), wbytes)
+    WS = rep(u8(ws), nW)
+    hh, rh, gh = synth.normal_bf16(1106, (K,)), synth.normal_bf16(1107, (K,), 0.0, 0.5), synth.normal_bf16(1108, (K,), 1.0, 0.1)
+    hd, rd, gd = bf(hh), bf(rh), bf(gh)
+    xn = torch.empty(K, dtype=torch.bfloat16, device=dev)
+    nr = torch.empty(K, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    us = time_launches(lambda i: fp8b.fp8_e4m3_rmsnorm_gemv(W[i], WS[i], hd, gd, rd), nW)
+    nbytes = wbytes + 3 * 2 * K + 2 * K + 2 * 2 * K + 2 * N
+    out["fp8_e4m3_rmsnorm_gemv residual+norm+wq_a 1536x4096 T=1"] = entry(us, nbytes, None)
+
+    def two_launches(i):
+        rb.rmsnorm_fuse_residual_add(hd, rd, gd, out_norm=xn, out_new_residual=nr)
+        fp8b.fp8_e4m3_gemv(W[i], WS[i], xn, out=y)
+
+    us = time_launches(two_launches, nW)
+    out["rmsnorm_fuse_residual_add + fp8_e4m3_gemv_m1 (two launches)"] = entry(us, nbytes, None)
+    del W, WS
     # RMSNorm + residual, H = 4096
     H = 4096
     g = synth.normal_bf16(1203, (H,), 1.0, 0.1)

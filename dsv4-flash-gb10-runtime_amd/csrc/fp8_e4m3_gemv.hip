@@ -245,6 +245,175 @@ __global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a, con
     }
 }
 
+// RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
+//   v = x + residual (fp32; or x alone), new_residual = bf16(v),
+//   x_norm = bf16( (g * bf16(v)) * rsqrt(sum(v^2) / K + eps) ),  y = W . x_norm
+// with the bits of librmsnorm_fuse's kernels: each of the 256 threads sums
+// the squares of the same 8-element chunks (t, t+256) in the same order,
+// the per-wave sums are added in wave order, and every element is normalised
+// by the same expression. The thread then normalises its own 16-element GEMV
+// slice and proceeds as fp8_gemv_tile_kernel. Workgroup 0 writes x_norm and
+// new_residual. The loads are issued activation, residual and weight-scale
+// slices first, then the weights, so the norm is computed while the weights
+// stream in.
+struct NormArgs {
+    const uint16_t* res;        // [T, K] or null
+    const uint16_t* g;          // [K]
+    float eps;
+    uint16_t* xnorm;            // [T, K]
+    uint16_t* new_res;          // [T, K] (with res)
+};
+
+__device__ __forceinline__ void unpack8_f32(const u32x4 v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+        f[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+    }
+}
+
+template <int C, int TT, int KC, bool RESID>
+__global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a, const NormArgs nm) {
+    constexpr int kRowsWG = C * 256 / KC;
+    constexpr int kVals = C * TT;
+    constexpr int kNV = KC / 128;               // 8-element chunks per thread in the norm's order
+    __shared__ float part[kWaves][C][TT];
+    __shared__ float red[TT][kWaves];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int n0 = blockIdx.x * kRowsWG;
+    const int k = 16 * (t % KC);
+    const int K = a.K;
+
+    // The norm's chunks, then the GEMV slice of x, residual and g.
+    u32x4 px[TT][kNV], pr[TT][kNV];
+    u32x4 sx[TT][2], sr[TT][2], sg[2];
+#pragma unroll
+    for (int tok = 0; tok < TT; ++tok) {
+        const int64_t row = (int64_t)min(tok, a.T - 1) * K;
+#pragma unroll
+        for (int c = 0; c < kNV; ++c) {
+            const int64_t e = row + 8 * (t + 256 * c);
+            px[tok][c] = *reinterpret_cast<const u32x4*>(a.x + e);
+            if constexpr (RESID) pr[tok][c] = *reinterpret_cast<const u32x4*>(nm.res + e);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            sx[tok][h] = *reinterpret_cast<const u32x4*>(a.x + row + k + 8 * h);
+            if constexpr (RESID) sr[tok][h] = *reinterpret_cast<const u32x4*>(nm.res + row + k + 8 * h);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sg[h] = *reinterpret_cast<const u32x4*>(nm.g + k + 8 * h);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 w[C];
+    uint32_t sb[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const int64_t gn = min(n0 + (t + 256 * i) / KC, a.N - 1);
+        w[i] = ld16_stream(a.w + gn * a.wrow + k);
+        sb[i] = a.s[(gn / kTile) * a.srow + k / kTile];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Sum of squares per token, in the order of rmsnorm_vec_kernel.
+#pragma unroll
+    for (int tok = 0; tok < TT; ++tok) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < kNV; ++c) {
+            float xa[8], ra[8];
+            unpack8_f32(px[tok][c], xa);
+            if constexpr (RESID) unpack8_f32(pr[tok][c], ra);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = RESID ? xa[e] + ra[e] : xa[e];
+                ss = fmaf(v, v, ss);
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[tok][wave] = ss;
+    }
+    __syncthreads();
+    const bool writer = blockIdx.x == 0 && t < KC;
+    uint32_t xp[TT][8];
+    float gf[16];
+    unpack8_f32(sg[0], gf);
+    unpack8_f32(sg[1], gf + 8);
+#pragma unroll
+    for (int tok = 0; tok < TT; ++tok) {
+        float total = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) total += red[tok][w2];
+        const float rms = rsqrtf(total * (1.0f / (float)K) + nm.eps);
+        float xa[16], ra[16];
+        unpack8_f32(sx[tok][0], xa);
+        unpack8_f32(sx[tok][1], xa + 8);
+        if constexpr (RESID) {
+            unpack8_f32(sr[tok][0], ra);
+            unpack8_f32(sr[tok][1], ra + 8);
+        }
+        uint16_t nb[16], tb[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float v = xa[e];
+            if constexpr (RESID) {
+                tb[e] = f32_to_bf16_bits(xa[e] + ra[e]);
+                v = bf16_bits_to_f32(tb[e]);
+            }
+            nb[e] = f32_to_bf16_bits((gf[e] * v) * rms);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xp[tok][q] = (uint32_t)nb[2 * q] | ((uint32_t)nb[2 * q + 1] << 16);
+        if (writer && tok < a.T) {
+            const int64_t o = (int64_t)tok * K + k;
+            u32x4 lo, hi;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                lo[q] = xp[tok][q];
+                hi[q] = xp[tok][4 + q];
+            }
+            *reinterpret_cast<u32x4*>(nm.xnorm + o) = lo;
+            *reinterpret_cast<u32x4*>(nm.xnorm + o + 8) = hi;
+            if constexpr (RESID) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    lo[q] = (uint32_t)tb[2 * q] | ((uint32_t)tb[2 * q + 1] << 16);
+                    hi[q] = (uint32_t)tb[8 + 2 * q] | ((uint32_t)tb[8 + 2 * q + 1] << 16);
+                }
+                *reinterpret_cast<u32x4*>(nm.new_res + o) = lo;
+                *reinterpret_cast<u32x4*>(nm.new_res + o + 8) = hi;
+            }
+        }
+    }
+
+    float acc[kVals];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const float sc = e8m0_to_f32(sb[i]);
+#pragma unroll
+        for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[i], xp[tok]) * sc;
+    }
+    wave_reduce_n<kVals>(acc, lane);
+    const int v = reduced_index<kVals>(lane);
+    if (reduced_owner<kVals>(lane)) part[wave][v / TT][v % TT] = acc[0];
+    __syncthreads();
+    for (int o = t; o < kRowsWG * TT; o += 256) {
+        const int r = o / TT;
+        const int tok = o % TT;
+        if (tok >= a.T || n0 + r >= a.N) continue;
+        float sum = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if ((64 * w2 + 256 * i) / KC == r) sum += part[w2][i][tok];
+        }
+        a.y[(int64_t)tok * a.ystride + n0 + r] = f32_to_bf16_bits(sum);
+    }
+}
+
 // One thread per 16 bytes of a row.
 __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* w, const uint8_t* s, int K,
                                                           int N, int64_t wrow, int64_t srow,
@@ -437,6 +606,52 @@ extern "C" int fp8_e4m3_dequant_bf16(const uint8_t* W_fp8, const uint8_t* W_scal
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         std::fprintf(stderr, "fp8_e4m3_dequant_bf16 launch failed: %s\n", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
+extern "C" int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* residual,
+                                     const dsv4_bf16_t* norm_weight, float eps, const uint8_t* W_fp8,
+                                     const uint8_t* W_scale, int K, int N, int T,
+                                     int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                                     dsv4_bf16_t* y, dsv4_bf16_t* x_norm, dsv4_bf16_t* new_residual,
+                                     hipStream_t stream) {
+    const int v = validate(K, N);
+    if (v != 0) return v;
+    if (T < 1 || T > 4) {
+        std::fprintf(stderr, "fp8_e4m3_rmsnorm_gemv: T=%d outside [1, 4]\n", T);
+        return -5;
+    }
+    Fp8Args a{reinterpret_cast<const uint16_t*>(x), K, W_fp8, W_scale, K, N, T,
+              weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y), N, 0, 0};
+    const bool ok = tile_ok(a) && norm_weight && x_norm && aligned16(norm_weight) && aligned16(x_norm) &&
+                    (!residual || (aligned16(residual) && new_residual && aligned16(new_residual)));
+    if (!ok) {
+        std::fprintf(stderr, "fp8_e4m3_rmsnorm_gemv: needs K in {2048, 4096}, 16-byte aligned operands, "
+                             "x_norm, and new_residual with a residual\n");
+        return -6;
+    }
+    const NormArgs nm{reinterpret_cast<const uint16_t*>(residual), reinterpret_cast<const uint16_t*>(norm_weight),
+                      eps, reinterpret_cast<uint16_t*>(x_norm), reinterpret_cast<uint16_t*>(new_residual)};
+    const int KC = K / 16;
+    const dim3 grid((unsigned)((N + 4 * 256 / KC - 1) / (4 * 256 / KC)));
+#define DSV4_NG(TTV, RES)                                                                                          \
+    if (KC == 256) hipLaunchKernelGGL((fp8_norm_gemv_tile_kernel<4, TTV, 256, RES>), grid, dim3(256), 0, stream, a, nm); \
+    else hipLaunchKernelGGL((fp8_norm_gemv_tile_kernel<4, TTV, 128, RES>), grid, dim3(256), 0, stream, a, nm);
+    if (residual) {
+        if (T == 1) { DSV4_NG(1, true) }
+        else if (T == 2) { DSV4_NG(2, true) }
+        else { DSV4_NG(4, true) }
+    } else {
+        if (T == 1) { DSV4_NG(1, false) }
+        else if (T == 2) { DSV4_NG(2, false) }
+        else { DSV4_NG(4, false) }
+    }
+#undef DSV4_NG
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "fp8_e4m3_rmsnorm_gemv launch failed: %s\n", hipGetErrorString(e));
         return -4;
     }
     return 0;

@@ -49,6 +49,8 @@ def _load_lib() -> ctypes.CDLL:
         lib.fp8_e4m3_gemv_grouped.restype = I
         lib.fp8_e4m3_swiglu_gemv.argtypes = [P, L, P, P, P, P, I, I, I, L, L, ctypes.c_float, I, P, L, P]
         lib.fp8_e4m3_swiglu_gemv.restype = I
+        lib.fp8_e4m3_rmsnorm_gemv.argtypes = [P, P, P, ctypes.c_float, P, P, I, I, I, L, L, P, P, P, P]
+        lib.fp8_e4m3_rmsnorm_gemv.restype = I
         _LIB = lib
     return _LIB
 
@@ -203,6 +205,47 @@ def fp8_e4m3_swiglu_gemv(
     if rc != 0:
         raise RuntimeError(f"fp8_e4m3_swiglu_gemv returned {rc}")
     return out
+
+
+def fp8_e4m3_rmsnorm_gemv(
+    W_fp8: torch.Tensor,
+    W_scale: torch.Tensor,
+    x: torch.Tensor,
+    norm_weight: torch.Tensor,
+    residual: Optional[torch.Tensor] = None,
+    eps: float = 1e-6,
+    stream: Optional[torch.cuda.Stream] = None,
+):
+    """RMSNorm (with the residual add when `residual` is given) and the FP8
+    GEMV that consumes it, in one launch. x, residual [K] or [T, K] (T <= 4),
+    K in {2048, 4096}. Returns (y, x_norm, new_residual or None), with the bits
+    of rmsnorm_fuse_residual_add / rmsnorm_fuse_fwd and fp8_e4m3_gemv."""
+    _check_w(W_fp8, W_scale)
+    N, K = W_fp8.shape
+    for name, t in (("x", x), ("norm_weight", norm_weight)) + ((("residual", residual),) if residual is not None else ()):
+        if not t.is_cuda or t.dtype != torch.bfloat16:
+            raise RuntimeError(f"{name} must be a GPU bfloat16 tensor")
+    if x.dim() not in (1, 2) or x.shape[-1] != K or norm_weight.shape != (K,):
+        raise RuntimeError(f"x must be [K] or [T, K] and norm_weight [K], K={K}")
+    if residual is not None and residual.shape != x.shape:
+        raise RuntimeError("residual must have the shape of x")
+    T = 1 if x.dim() == 1 else x.shape[0]
+    x = x.contiguous()
+    norm_weight = norm_weight.contiguous()
+    y = torch.empty((N,) if x.dim() == 1 else (T, N), dtype=torch.bfloat16, device=x.device)
+    x_norm = torch.empty_like(x)
+    new_res = None
+    if residual is not None:
+        residual = residual.contiguous()
+        new_res = torch.empty_like(x)
+    rc = _load_lib().fp8_e4m3_rmsnorm_gemv(
+        _lib.vp(x), _lib.vp(residual) if residual is not None else None, _lib.vp(norm_weight), float(eps),
+        _lib.vp(W_fp8), _lib.vp(W_scale), K, N, T, W_fp8.stride(0), W_scale.stride(0), _lib.vp(y),
+        _lib.vp(x_norm), _lib.vp(new_res) if new_res is not None else None,
+        ctypes.c_void_p(_lib.stream_ptr(x.device, stream)))
+    if rc != 0:
+        raise RuntimeError(f"fp8_e4m3_rmsnorm_gemv returned {rc}")
+    return y, x_norm, new_res
 
 
 def fp8_e4m3_dequant(W_fp8: torch.Tensor, W_scale: torch.Tensor,

@@ -12,7 +12,7 @@
  *                                                 mxfp4_dequant_bf16 (extension)
  *   kernel/fp8-dense/libfp8_e4m3_gemv.so          fp8_e4m3_gemv_m1,
  *                                                 fp8_e4m3_gemv, fp8_e4m3_gemv_grouped,
- *                                                 fp8_e4m3_swiglu_gemv,
+ *                                                 fp8_e4m3_swiglu_gemv, fp8_e4m3_rmsnorm_gemv,
  *                                                 fp8_e4m3_dequant_bf16 (extensions)
  *   kernel/rmsnorm-fuse/librmsnorm_fuse.so        rmsnorm_fuse_fwd,
  *                                                 rmsnorm_fuse_residual_add
@@ -234,6 +234,27 @@ int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8
                          int K, int N, int T, int64_t weight_row_stride_bytes,
                          int64_t scale_row_stride_bytes, float limit, int clamp_up,
                          dsv4_bf16_t* act, int64_t act_row_stride, hipStream_t stream);
+
+/* EXTENSION (folds the RMSNorm launch into the GEMV that consumes it; the
+ * reference runs rmsnorm then FP8 GEMVs as separate launches,
+ * kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:395-418 and
+ * kernel/rmsnorm-fuse/rmsnorm_fuse.cu:110-157): one launch for
+ *   v = x + residual (fp32; v = x when residual is NULL)
+ *   new_residual = bf16(v)                                  (with a residual)
+ *   x_norm = bf16( (norm_weight * bf16(v)) * rsqrt(sum(v^2)/K + eps) )
+ *   y = bf16( W . x_norm )                                   (as fp8_e4m3_gemv)
+ * for T token rows; x, residual, x_norm, new_residual are [T, K] contiguous,
+ * y [T, N] contiguous. x_norm and new_residual have the bits of
+ * rmsnorm_fuse_fwd / rmsnorm_fuse_residual_add, y those of fp8_e4m3_gemv on
+ * x_norm. Needs K in {2048, 4096}, T in [1, 4] (-5), 16-byte aligned
+ * operands and x_norm (and new_residual with a residual) (-6). Returns as
+ * fp8_e4m3_gemv otherwise. */
+int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* residual,
+                          const dsv4_bf16_t* norm_weight, float eps, const uint8_t* W_fp8,
+                          const uint8_t* W_scale, int K, int N, int T,
+                          int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
+                          dsv4_bf16_t* y, dsv4_bf16_t* x_norm, dsv4_bf16_t* new_residual,
+                          hipStream_t stream);
 
 /* EXTENSION (debug): out[n,k] = bf16( e4m3(W[n,k]) * 2^(S[n/128,k/128]-127) ),
  * the device decode of the FP8 GEMVs, for the bit-exact check against

@@ -23,7 +23,7 @@ LIBS = {
         "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
-                                      "fp8_e4m3_swiglu_gemv", "fp8_e4m3_dequant_bf16"],
+                                      "fp8_e4m3_swiglu_gemv", "fp8_e4m3_rmsnorm_gemv", "fp8_e4m3_dequant_bf16"],
     "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],
 }
 
@@ -210,6 +210,13 @@ def test_fp8_validation_codes():
     assert sw(N, 4096, N, N, N, N, 4000, 2048, 1, 4096, 32, 10.0, 1, N, 2048, N) == -1
     # K = 1024 is a valid GEMV shape that the fused kernel does not take
     assert sw(N, 1024, N, N, N, N, 1024, 2048, 1, 1024, 8, 10.0, 1, N, 2048, N) == -6
+    rn = lib.fp8_e4m3_rmsnorm_gemv
+    rn.restype = I
+    rn.argtypes = [P, P, P, ctypes.c_float, P, P, I, I, I, L, L, P, P, P, P]
+    assert rn(N, N, N, 1e-6, N, N, 4096, 1536, 5, 4096, 32, N, N, N, N) == -5
+    assert rn(N, N, N, 1e-6, N, N, 4000, 1536, 1, 4096, 32, N, N, N, N) == -1
+    assert rn(N, N, N, 1e-6, N, N, 1024, 1536, 1, 1024, 8, N, N, N, N) == -6
+    assert rn(N, N, N, 1e-6, N, N, 4096, 1536, 1, 4096, 32, N, None, N, N) == -6  # no x_norm
 
 
 def test_rmsnorm_validation_codes():

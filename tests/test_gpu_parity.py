@@ -204,6 +204,36 @@ def test_fp8_swiglu_gemv(device, N, K, T, clamp_up):
     assert_close(act, mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, clamp_up), f"fp8 swiglu T={T}")
 
 
+@pytest.mark.parametrize("N,K,T,resid", [(1536, 4096, 1, True), (576, 4096, 1, False), (300, 2048, 3, True),
+                                         (4096, 4096, 4, True), (77, 2048, 2, False)])
+def test_fp8_rmsnorm_gemv(device, N, K, T, resid):
+    """RMSNorm (+ residual) folded into the FP8 GEMV: x_norm and new_residual
+    are the bits of the RMSNorm library, y the bits of fp8_e4m3_gemv on x_norm,
+    and all match the oracle."""
+    announce(f"fp8_e4m3_rmsnorm_gemv N={N} K={K} T={T} residual={resid}")
+    w, s = synth.fp8_weight(4800 + N, N, K)
+    h = synth.normal_bf16(4801 + T, (T, K))
+    r = synth.normal_bf16(4802 + T, (T, K), 0.0, 0.5)
+    g = synth.normal_bf16(4803, (K,), 1.0, 0.1)
+    tw, ts = dev_u8(w, device), dev_u8(s, device)
+    hd, rd, gd = dev_bf16(h, device), dev_bf16(r, device), dev_bf16(g, device)
+    y, xn, nr = fp8b.fp8_e4m3_rmsnorm_gemv(tw, ts, hd if T > 1 else hd[0], gd,
+                                           (rd if T > 1 else rd[0]) if resid else None)
+    if resid:
+        ref_xn, ref_nr = rb.rmsnorm_fuse_residual_add(hd, rd, gd)
+        assert np.array_equal(host_bits(nr).reshape(T, K), host_bits(ref_nr)), "new_residual bits"
+        oracle_xn, oracle_nr = mx.rmsnorm_residual(h, r, g)
+        assert np.array_equal(host_bits(nr).reshape(T, K), oracle_nr)
+    else:
+        ref_xn = rb.rmsnorm_fuse_fwd(hd, gd)
+        oracle_xn = mx.rmsnorm(h, g)
+    assert np.array_equal(host_bits(xn).reshape(T, K), host_bits(ref_xn)), "x_norm bits"
+    ref_y = fp8b.fp8_e4m3_gemv(tw, ts, ref_xn if T > 1 else ref_xn.view(-1))
+    assert np.array_equal(host_bits(y).reshape(T, N), host_bits(ref_y).reshape(T, N)), "y bits"
+    assert_close(host_bits(xn).reshape(T, K), oracle_xn, "x_norm vs oracle")
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(oracle_xn, w, s), "y vs oracle")
+
+
 # ------------------------------------------------------ grouped (drop-in) --
 
 def _packed_experts(seed, n, K, H, O):
