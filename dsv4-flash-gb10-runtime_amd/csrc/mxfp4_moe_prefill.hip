@@ -278,6 +278,7 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
         const int q = t + 256 * i;
         if (q < (TWO ? 2 : 1) * spieces) slv[q] = sv[i];
     }
+    __syncthreads();  // the scale tile is read before each step's barrier
     const uint8_t* sla = sl + rl * nblk + g;               // + 4*s: this lane's block of super-step s
     const uint8_t* slb = sl + spieces * 16 + rl * nblk + g;
 
@@ -301,12 +302,15 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
             u32x4 wb_c{};
             if constexpr (TWO) wb_c = wb_r[d];
             load_w(d, s + DW);
-            __syncthreads();
+            // The dequantisation needs only this wave's registers and the
+            // scale tile, so it runs before the barrier and overlaps the wait
+            // for the other waves' activation pieces.
             const uint32_t sa_c = sla[4 * s];
             const uint32_t sb_c = TWO ? slb[4 * s] : 0u;
             bf16x8 opa[4], opb[4];
             dequant_block(wa_c, sa_c, opa);
             if constexpr (TWO) dequant_block(wb_c, sb_c, opb);
+            __syncthreads();
 #pragma unroll
             for (int b = 0; b < NTB; ++b) {
                 const uint16_t* xrow = xb + (16 * b + (lane & 15)) * kLdsRow + 32 * g;
