@@ -309,8 +309,10 @@ def route_sigmoid_topk(logits, topk: int):
     l = np.asarray(logits, dtype=np.float32)
     ids = np.argsort(-l.astype(np.float64), axis=1, kind="stable")[:, :topk].astype(np.int32)
     sel = np.take_along_axis(l, ids, axis=1).astype(np.float64)
-    s = 1.0 / (1.0 + np.exp(-sel))
-    return ids, (s / s.sum(axis=1, keepdims=True)).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        s = 1.0 / (1.0 + np.exp(-sel))
+        # a token whose selected logits are all -inf gets 0/0 = NaN weights
+        return ids, (s / s.sum(axis=1, keepdims=True)).astype(np.float32)
 
 
 # ---------------------------------------------------------------- RMSNorm ---
