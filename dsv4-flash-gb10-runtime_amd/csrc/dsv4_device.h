@@ -256,6 +256,19 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return wave_allreduce_u32(v, [](uint32_t a, uint32_t b) { return max(a, b); });
 }
 
+// Maximum over the wave as a wave-uniform value: the four DPP steps reduce
+// each 16-lane row, then the four row results meet through readlane and
+// scalar max (shorter than the two permlane swaps plus a readfirstlane).
+__device__ __forceinline__ uint32_t wave_max_u32_uniform(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
 // Order-preserving key of a non-NaN float: a > b exactly when key(a) >
 // key(b), except that -0 and +0 get different keys (callers map -0 to +0).
 __device__ __forceinline__ uint32_t order_key(float f) {

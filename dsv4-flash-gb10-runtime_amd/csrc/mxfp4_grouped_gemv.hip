@@ -196,15 +196,78 @@ __device__ __forceinline__ float scale_of(uint32_t packed, int j) {
     return e8m0_to_f32((packed >> (8 * j)) & 0xFFu);
 }
 
+// Selection rounds over keys held 4 per lane (key 0 = absent or taken; slot
+// i of lane l is expert l + 64*i). Each lane first sorts its keys, largest
+// first, with an odd-even transposition network that swaps only strictly
+// out-of-order neighbours, so equal keys keep their slot order. A round then
+// reduces one head per lane, and one ballot names the lanes whose head is the
+// maximum: a single such lane holds the pick (its head is the lowest slot
+// among its equal keys); with several (equal logits), a wave min over
+// 64*slot + lane of their heads finds the lowest expert index, on a
+// wave-uniform branch. The winner shifts its list up by one. KFIX > 0 fixes
+// the trip count at compile time (topk == KFIX), which unrolls the rounds.
+template <int KFIX>
+__device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int topk, int lane, int& me,
+                                                  uint32_t& mk) {
+    uint32_t k[4], s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        k[i] = kv[i];
+        s[i] = i;
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+#pragma unroll
+        for (int i = p & 1; i + 1 < 4; i += 2) {
+            const bool sw = k[i + 1] > k[i];
+            const uint32_t ka = sw ? k[i + 1] : k[i], kb = sw ? k[i] : k[i + 1];
+            const uint32_t sa = sw ? s[i + 1] : s[i], sb = sw ? s[i] : s[i + 1];
+            k[i] = ka;
+            k[i + 1] = kb;
+            s[i] = sa;
+            s[i + 1] = sb;
+        }
+    }
+    auto round = [&](int r) {
+        const uint32_t m = wave_max_u32_uniform(k[0]);
+        const uint64_t b = __ballot(k[0] == m);
+        int idx;
+        if (__builtin_popcountll(b) == 1) {
+            const int l = __builtin_ctzll(b);
+            idx = 64 * __builtin_amdgcn_readlane(s[0], l) + l;
+        } else {
+            idx = __builtin_amdgcn_readfirstlane(
+                wave_min_i32(k[0] == m ? (int)(64 * s[0]) + lane : 0x7FFFFFFF));
+        }
+        const bool hit = lane == (idx & 63);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            k[i] = hit ? k[i + 1] : k[i];
+            s[i] = hit ? s[i + 1] : s[i];
+        }
+        k[3] = hit ? 0u : k[3];
+        me = lane == r ? idx : me;
+        mk = lane == r ? m : mk;
+    };
+    if constexpr (KFIX > 0) {
+#pragma unroll
+        for (int r = 0; r < KFIX; ++r) round(r);
+    } else {
+        for (int r = 0; r < topk; ++r) round(r);
+    }
+}
+
 // Top-k of one token's logits on one wave: descending, ties to the lower
 // expert index, weights sigmoid(l) renormalised to sum 1. Lane k < topk
 // returns the k-th pick. Each lane holds PER logits (expert lane + 64*i) as
 // order-preserving integer keys (larger logit <-> larger key; -0 is taken as
 // +0 and NaN as -inf, so equal logits give equal keys); entries past
-// n_experts and picked entries are key 0, below every logit. Each round is
-// one integer max reduction; the winner's index comes from one ballot per
-// element slot (lowest slot first, then lowest lane: the lowest expert
-// index among equal keys) and is removed by a select.
+// n_experts and picked entries are key 0, below every logit. With up to 256
+// experts (PER 4) the rounds run on sorted per-lane lists
+// (topk_sorted_heads). Otherwise each round is one integer max reduction over
+// every key; the winner's index comes from one ballot per element slot
+// (lowest slot first, then lowest lane: the lowest expert index among equal
+// keys) and is removed by a select.
 template <int PER>
 __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk,
                                                   int lane, int& my_e, float& my_w) {
@@ -225,7 +288,10 @@ __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts
     }
     int me = 0;
     uint32_t mk = 0;
-    for (int k = 0; k < topk; ++k) {
+    if constexpr (PER == 4) {
+        if (topk == 8) topk_sorted_heads<8>(kv, topk, lane, me, mk);
+        else topk_sorted_heads<0>(kv, topk, lane, me, mk);
+    } else for (int k = 0; k < topk; ++k) {
         uint32_t best = kv[0];
 #pragma unroll
         for (int i = 1; i < PER; ++i) best = max(best, kv[i]);
