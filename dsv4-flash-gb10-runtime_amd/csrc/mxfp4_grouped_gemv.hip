@@ -204,10 +204,12 @@ __device__ __forceinline__ float scale_of(uint32_t packed, int j) {
 // maximum: a single such lane holds the pick (its head is the lowest slot
 // among its equal keys); with several (equal logits), a wave min over
 // 64*slot + lane of their heads finds the lowest expert index, on a
-// wave-uniform branch. The winner shifts its list up by one. KFIX > 0 fixes
-// the trip count at compile time (topk == KFIX), which unrolls the rounds.
+// wave-uniform branch. The winner shifts its list up by one. Only the first
+// `rounds` picks are made. KFIX > 0 bounds the rounds at compile time
+// (rounds <= KFIX), which unrolls them; each unrolled round is skipped by a
+// wave-uniform branch once `rounds` are done.
 template <int KFIX>
-__device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int topk, int lane, int& me,
+__device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int rounds, int lane, int& me,
                                                   uint32_t& mk) {
     uint32_t k[4], s[4];
 #pragma unroll
@@ -251,9 +253,10 @@ __device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int t
     };
     if constexpr (KFIX > 0) {
 #pragma unroll
-        for (int r = 0; r < KFIX; ++r) round(r);
+        for (int r = 0; r < KFIX; ++r)
+            if (r < rounds) round(r);
     } else {
-        for (int r = 0; r < topk; ++r) round(r);
+        for (int r = 0; r < rounds; ++r) round(r);
     }
 }
 
@@ -268,8 +271,11 @@ __device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int t
 // every key; the winner's index comes from one ballot per element slot
 // (lowest slot first, then lowest lane: the lowest expert index among equal
 // keys) and is removed by a select.
+// `rounds` (1..topk, wave-uniform) stops after the first `rounds` picks: lanes
+// at or past it return expert 0. The weights need every pick, so they are
+// computed only when rounds == topk (my_w is 0 otherwise).
 template <int PER>
-__device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk,
+__device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk, int rounds,
                                                   int lane, int& my_e, float& my_w) {
     // Unconditional loads (index clamped into the row), all in flight
     // together: the empty asm keeps the compiler from moving a load into the
@@ -289,9 +295,9 @@ __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts
     int me = 0;
     uint32_t mk = 0;
     if constexpr (PER == 4) {
-        if (topk == 8) topk_sorted_heads<8>(kv, topk, lane, me, mk);
-        else topk_sorted_heads<0>(kv, topk, lane, me, mk);
-    } else for (int k = 0; k < topk; ++k) {
+        if (topk == 8) topk_sorted_heads<8>(kv, rounds, lane, me, mk);
+        else topk_sorted_heads<0>(kv, rounds, lane, me, mk);
+    } else for (int k = 0; k < rounds; ++k) {
         uint32_t best = kv[0];
 #pragma unroll
         for (int i = 1; i < PER; ++i) best = max(best, kv[i]);
@@ -311,16 +317,19 @@ __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts
         mk = lane == k ? m : mk;
     }
     my_e = me;
-    const float my_l = lane < topk ? key_value(mk) : -INFINITY;
-    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
-    my_w = s / wave_sum_f32(s);
+    my_w = 0.f;
+    if (rounds == topk) {
+        const float my_l = lane < topk ? key_value(mk) : -INFINITY;
+        const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
+        my_w = s / wave_sum_f32(s);
+    }
 }
 
-__device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int lane,
-                                              int& e, float& w) {
-    if (n_experts <= 256) wave_topk_sigmoid<4>(lt, n_experts, topk, lane, e, w);
-    else if (n_experts <= 512) wave_topk_sigmoid<8>(lt, n_experts, topk, lane, e, w);
-    else wave_topk_sigmoid<16>(lt, n_experts, topk, lane, e, w);
+__device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int rounds,
+                                              int lane, int& e, float& w) {
+    if (n_experts <= 256) wave_topk_sigmoid<4>(lt, n_experts, topk, rounds, lane, e, w);
+    else if (n_experts <= 512) wave_topk_sigmoid<8>(lt, n_experts, topk, rounds, lane, e, w);
+    else wave_topk_sigmoid<16>(lt, n_experts, topk, rounds, lane, e, w);
 }
 
 // ---------------------------------------------------------------- stage A --
@@ -633,13 +642,16 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     } else if constexpr (GATE == 1) {
         // Wave 0 ranks the logits (the same computation in every workgroup);
         // workgroup (0, 0) publishes the routing for stage B and the caller.
+        // The other workgroups stop after pick blockIdx.y, the one they serve.
         if (wave == 0) {
             const GateArgs& g = a.gate;
+            const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
             int e;
             float w;
-            wave_topk_any(g.logits, g.n_experts, g.topk, lane, e, w);
+            wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e,
+                          w);
             if (lane < g.topk) s_pick[lane] = e;
-            if (blockIdx.x == 0 && blockIdx.y == 0 && lane < g.topk) {
+            if (publish && lane < g.topk) {
                 if (g.ids_out != nullptr) {
                     g.ids_out[lane] = e;
                     g.w_out[lane] = w;
@@ -1395,7 +1407,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
         for (int t = wave; t < T; t += kRouteThreads / 64) {
             int e;
             float w;
-            wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, lane, e, w);
+            wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, topk, lane, e, w);
             if (lane < topk) {
                 sid[t * topk + lane] = e;
                 sw[t * topk + lane] = w;
@@ -1505,7 +1517,7 @@ __global__ __launch_bounds__(64) void moe_route_sigmoid_topk_kernel(const float*
     const int lane = threadIdx.x;
     int e;
     float w;
-    wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, lane, e, w);
+    wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, topk, lane, e, w);
     if (lane < topk) {
         ids[(int64_t)t * topk + lane] = e;
         wout[(int64_t)t * topk + lane] = w;
