@@ -7,8 +7,14 @@ routing tables, then stage A (W1/W3 + SiLU) and stage B (W2 + weighted combine)
 of the expert-indexed MXFP4 grouped GEMV. At T=1 the gating runs inside stage A
 (two launches); for T>1 it is a launch of its own. The kernels read the routed
 experts in place from HBM-resident per-layer tensors. The
-K timed steps are captured once in a HIP graph and replayed (the eager,
-host-issued timing of the same steps is reported beside it). Inputs are resident in HBM before the timed region. Steps
+K timed steps are timed twice, each time over all K steps: issued from the
+host loop (two or three launches per step on one stream), and captured in a
+HIP graph and replayed. The faster of the two is the headline (`timing` names
+it) and both are reported: on this ROCm build a replayed graph leaves more
+time between dependent kernels than host-issued launches at T=1 (the layer
+measured 23.4-23.7 against 24.1-25.0 us), while a host loop that issues many
+launches per step (config 4) is bound by the host. Inputs are resident in HBM
+before the timed region. Steps
 cycle over --layers layers of 256 experts (4 x 3.42 GB by default) with fresh
 logits each step, so weights come from HBM, not the 256 MB MALL.
 
@@ -260,7 +266,8 @@ def config4(args, torch, dev) -> dict:
     token per layer by Gumbel-top-8 on log p (runtime.synth.zipf_routing) with
     sigmoid(N(0,1)) weights renormalised. One step = the 43 routed MoE layers
     (expert-indexed grouped GEMV, caller-given ids); the --steps steps are
-    captured in one HIP graph and replayed."""
+    captured in one HIP graph and replayed, and separately issued from the
+    host loop; the faster is the headline."""
     from runtime import moe, synth
 
     L4 = args.layers if args.layers != 4 else 43
@@ -296,7 +303,17 @@ def config4(args, torch, dev) -> dict:
     graph.replay()
     ev1.record()
     torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / S
+    ms_graph = ev0.elapsed_time(ev1) / S
+    del graph
+    log(f"configs[4]: timing {S} steps issued from the host")
+    torch.cuda.synchronize()
+    ev0.record()
+    for i in range(args.warmup, args.warmup + S):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms_host = ev0.elapsed_time(ev1) / S
+    ms = min(ms_graph, ms_host)
     uniq = sum(len(np.unique(ids_h[l][i])) for l in range(L4) for i in range(args.warmup, args.warmup + S))
     step_bytes = uniq / S * EXPERT_BYTES + L4 * (2 * K * 2 + TOPK * 8)
     gbs = step_bytes / (ms * 1e-3) / 1e9
@@ -355,8 +372,12 @@ def config4(args, torch, dev) -> dict:
                                f"({L4 * E * EXPERT_BYTES / 1e9:.1f} GB)",
                    "layers": L4, "tokens": 1, "experts": E, "topk": TOPK,
                    "algorithmic_bytes_per_step": int(step_bytes)},
+        "timing": ("HIP graph replay" if ms_graph <= ms_host else "launches issued from the host loop")
+                  + " (the faster of the two; HIP events on the launch stream)",
         "us_per_layer": round(ms * 1e3 / L4, 3),
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "us_per_layer_graph": round(ms_graph * 1e3 / L4, 3),
+        "us_per_layer_host_issued": round(ms_host * 1e3 / L4, 3),
         "prefill": prefill,
     }
 
@@ -447,14 +468,16 @@ def main() -> int:
     graph.replay()
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps (graph replay)")
-    ms_per_step = timed(graph.replay) / args.steps
-    log(f"timing {args.steps} steps (eager)")
+    ms_per_step_graph = timed(graph.replay) / args.steps
+    del graph
+    log(f"timing {args.steps} steps (issued from the host)")
 
     def eager():
         for i in range(args.warmup, n_steps):
             step(i)
 
-    ms_per_step_eager = timed(eager) / args.steps
+    ms_per_step_host = timed(eager) / args.steps
+    ms_per_step = min(ms_per_step_host, ms_per_step_graph)
     timed_bytes = float(step_bytes[args.warmup:].mean())
     value = timed_bytes / (ms_per_step * 1e-3) / 1e9
 
@@ -588,8 +611,12 @@ def main() -> int:
             "mean_unique_experts": round(float(uniq[args.warmup:].mean()), 3),
             "algorithmic_bytes_per_step": int(round(timed_bytes)),
         },
+        "timing": ("HIP graph replay" if ms_per_step_graph <= ms_per_step_host
+                   else "launches issued from the host loop")
+                  + " (the faster of the two over the same K steps; HIP events on the launch stream)",
         "moe_layer_us": round(ms_per_step * 1e3, 3),
-        "moe_layer_us_eager": round(ms_per_step_eager * 1e3, 3),
+        "moe_layer_us_graph": round(ms_per_step_graph * 1e3, 3),
+        "moe_layer_us_host_issued": round(ms_per_step_host * 1e3, 3),
         "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         "copy_ceiling_gbs": round(copy_gbs, 1),
         "stage_us": {"swiglu_A": round(a_us, 3), "down_B": round(b_us, 3)},
