@@ -569,7 +569,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     constexpr int kSPer = (kSTile / 16 + kThreads - 1) / kThreads;     // 16-byte scale pieces per thread
     __shared__ u32x4 xl[kMaxRed * 2 / 16];
     __shared__ u32x4 sl[kSTile / 16];
-    __shared__ int s_pick[GATE ? kMaxTopk : 1];
+    __shared__ int s_pick[GATE == 2 ? kMaxTopk : 1];
     __shared__ int s_nu[1];
     const uint8_t* slb = reinterpret_cast<const uint8_t*>(sl);
     const int lane = threadIdx.x & 63;
@@ -640,35 +640,32 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         pbeg = blockIdx.y;
         valid = (int)blockIdx.y < s_nu[0];
     } else if constexpr (GATE == 1) {
-        // Wave 0 ranks the logits (the same computation in every workgroup);
-        // workgroup (0, 0) publishes the routing for stage B and the caller.
-        // The other workgroups stop after pick blockIdx.y, the one they serve.
-        if (wave == 0) {
-            const GateArgs& g = a.gate;
-            const bool publish = blockIdx.x == 0 && blockIdx.y == 0;
-            int e;
-            float w;
-            wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e,
-                          w);
-            if (lane < g.topk) s_pick[lane] = e;
-            if (publish && lane < g.topk) {
-                if (g.ids_out != nullptr) {
-                    g.ids_out[lane] = e;
-                    g.w_out[lane] = w;
-                }
-                g.rt.uexp[lane] = e;
-                g.rt.off[lane] = lane;
-                g.rt.pair_tok[lane] = 0;
-                g.rt.pair_w[lane] = w;
-                if (lane == 0) {
-                    g.rt.header[0] = g.topk;
-                    g.rt.header[1] = g.topk;
-                    g.rt.off[g.topk] = g.topk;
-                }
+        // Every wave ranks the logits itself (the same computation in every
+        // wave of every workgroup), so no wave waits on another before its
+        // weight loads; each stops after pick blockIdx.y, the one its
+        // workgroup serves. Wave 0 of workgroup (0, 0) ranks all k and
+        // publishes the routing for stage B and the caller.
+        const GateArgs& g = a.gate;
+        const bool publish = blockIdx.x == 0 && blockIdx.y == 0 && wave == 0;
+        int e;
+        float w;
+        wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e, w);
+        if (publish && lane < g.topk) {
+            if (g.ids_out != nullptr) {
+                g.ids_out[lane] = e;
+                g.w_out[lane] = w;
+            }
+            g.rt.uexp[lane] = e;
+            g.rt.off[lane] = lane;
+            g.rt.pair_tok[lane] = 0;
+            g.rt.pair_w[lane] = w;
+            if (lane == 0) {
+                g.rt.header[0] = g.topk;
+                g.rt.header[1] = g.topk;
+                g.rt.off[g.topk] = g.topk;
             }
         }
-        __syncthreads();
-        expert = s_pick[blockIdx.y];
+        expert = __builtin_amdgcn_readlane(e, (int)blockIdx.y);
         pbeg = blockIdx.y;
         valid = true;
     } else {
