@@ -334,6 +334,38 @@ def test_route_sigmoid_topk_edges(device, name, logits, k):
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-6, equal_nan=True), name
 
 
+@pytest.mark.parametrize("name,logits,k", _gating_edge_logits(), ids=lambda v: v if isinstance(v, str) else "")
+def test_moe_layer_one_token_gating_edges(device, name, logits, k):
+    """The one-token layer ranks the logits inside stage A: every wave of every
+    workgroup ranks them itself and stops after the pick its workgroup serves,
+    and one wave ranks all k and publishes ids, weights and stage B's tables.
+    On the edge sets each row, as a one-token call, must give the oracle's ids
+    and weights, and the layer output must match the oracle on those ids."""
+    logits = np.asarray(logits, dtype=np.float32)
+    E = logits.shape[1]
+    K, H, O = 2048, (32 if E > 256 else 64), 128        # K = 2048: the one-token kernel's shape
+    announce(f"mxfp4_moe_layer one-token gating edge case {name} E={E} k={k} K={K} H={H} O={O}")
+    mats = _packed_experts(9700 + E, E, K, H, O)
+    W1p, W3p, W2p, W1s, W3s, W2s = mats
+    W1, W3, W2 = _dev_mats(device, *mats)
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    for t in range(logits.shape[0]):
+        x = synth.normal_bf16(9800 + t, (1, K))
+        ids_out = torch.empty(1, k, dtype=torch.int32, device=device)
+        w_out = torch.empty(1, k, dtype=torch.float32, device=device)
+        out = gb.mxfp4_moe_layer(dev_bf16(x, device), dev_f32(logits[t:t + 1], device), W1, W3, W2, k,
+                                 ids_out=ids_out, weights_out=w_out)
+        rids, rw = mx.route_sigmoid_topk(logits[t:t + 1], k)
+        assert np.array_equal(ids_out.cpu().numpy(), rids), f"{name} row {t}"
+        # a row whose logits are all -inf gets 0/0 weights in both; its output is not compared
+        assert np.allclose(w_out.cpu().numpy(), rw, rtol=1e-5, atol=1e-6, equal_nan=True), f"{name} row {t}"
+        if np.all(np.isfinite(rw)):
+            assert_close(host_bits(out), mx.moe_layer(x, fn, rids, rw, O, n_experts=E), f"{name} row {t}")
+
+
 @pytest.mark.parametrize("T", [1, 4, 16])
 def test_moe_indexed_small_dims(device, T):
     """All T of the config at reduced K/H/O so the oracle covers every expert quickly."""
