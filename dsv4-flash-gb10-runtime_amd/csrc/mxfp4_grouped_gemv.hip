@@ -1251,7 +1251,8 @@ __global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_t1_kernel(c
 // workgroup owns RB output rows; wave w takes expert slots w, w+WB, ...) with
 // twice the bytes in flight per wave. Lane i of a wave first reads the
 // routing entries of the wave's slot i (expert, pair range, first pair's
-// token and weight: two round trips for all slots). Each step then issues
+// token and weight: two round trips for all slots, the rows waiting only for
+// the first). Each step then issues
 // the loads of two slots at once (2*RB rows) and reduces them in order.
 // Further pairs of a slot (an expert routed by several tokens) load their M
 // slice on demand. Partial sums per (wave, token, row) meet in LDS and are
@@ -1267,20 +1268,22 @@ __global__ __launch_bounds__(64 * WB, 4) void moe_down_tn_kernel(const StageBArg
     const int nblk = a.hidden / kBlkElems;     // 64
     const int64_t wrow = a.hidden / 2;
     const ExpertSet& es = a.es;
-    {
-        float* accf = &acc[0][0][0];
-        for (int i = threadIdx.x; i < WB * TM * RB; i += 64 * WB) accf[i] = 0.f;
-    }
+    // Each wave zeroes its own partial sums, so no barrier precedes the
+    // loads (a barrier would wait for every table load first).
+    for (int i = lane; i < TM * RB; i += 64) (&acc[wave][0][0])[i] = 0.f;
 
+    // The slot count and the wave's table entries are read in one round trip
+    // (entries are clamped to valid indices; those past the routed slots are
+    // never used); the first pair's token and weight take a second one, which
+    // the first slot's loads do not wait for.
+    const int su = min(wave + WB * lane, es.n_slots - 1);
     const int U = min(*es.n_unique, es.n_slots);
-    const int ns = U > wave ? (U - wave + WB - 1) / WB : 0;  // this wave's slots (<= 64, host-checked)
-    const int su = min(wave + WB * lane, max(U - 1, 0));
     const int e_l = min(max(es.uexp[su], 0), es.n_experts - 1);
     const int pb_l = min(max(es.off[su], 0), es.n_pairs - 1);
     const int pe_l = min(max(es.off[su + 1], pb_l + 1), es.n_pairs);
+    const int ns = U > wave ? (U - wave + WB - 1) / WB : 0;  // this wave's slots (<= 64, host-checked)
     const int tok_l = min(max(es.pair_tok[pb_l], 0), a.T - 1);
     const float w_l = es.pair_w[pb_l];
-    __syncthreads();  // acc zeroed
 
     using SPiece = typename ScalePiece<RB>::type;
     struct Rows {
