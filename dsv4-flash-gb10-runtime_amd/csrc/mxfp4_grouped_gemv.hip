@@ -378,8 +378,10 @@ struct StageAArgs {
 };
 
 // HC hidden rows of W1 and of W3 in registers: NB 16-byte blocks per lane per
-// row (lane l owns blocks NB*l .. NB*l+NB-1, so its activation slice and its
-// scale bytes are contiguous) plus the rows' packed scale bytes.
+// row plus the rows' packed scale bytes. The generic kernel gives lane l
+// blocks NB*l .. NB*l+NB-1 (contiguous activation slice and scale bytes); the
+// one-token and multi-token kernels give it blocks l, l+64, ... (each load
+// instruction of a wave then reads one contiguous KiB of a row).
 template <int NB, int HC>
 struct GateUpChunk {
     u32x4 w1[HC][NB];
