@@ -159,13 +159,15 @@ struct GemmArgs {
 
 // 16 bytes of e2m1 codes (one MX block) -> 32 bf16 in 4 operands of 8
 // (elements 8j..8j+7 in op[j]), times the block scale 2^(s-127) applied by
-// the conversion itself (exact). Scale byte 0xFF decodes to 0.
+// the conversion itself (exact for bytes 1..254). Scale byte 0xFF decodes to
+// a scale of 0, and so does byte 0 (2^-127 is an fp32 subnormal): every
+// element is then a zero, whose sign cannot change an fp32 sum that starts
+// at +0.
 __device__ __forceinline__ void dequant_block(u32x4 w, uint32_t s, bf16x8* op) {
-    const bool nan_scale = s == 0xFFu;
-    const float scale = __uint_as_float(nan_scale ? 0x3F800000u : (s << 23));
+    const float scale = __uint_as_float(s == 0xFFu ? 0u : (s << 23));
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t d = nan_scale ? 0u : w[q];
+        const uint32_t d = w[q];
         const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
         const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
         const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
