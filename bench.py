@@ -408,7 +408,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
-              "(the routed MoE would shard by experts or by the ff dimension; see DESIGN.md)",
+              "(the routed MoE would shard by experts, or by the ff dimension with one all-reduce "
+              "of the layer output per step)",
               file=sys.stderr)
         return 2
 

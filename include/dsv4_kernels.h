@@ -137,7 +137,8 @@ int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
                     hipStream_t stream);
 
 /* EXTENSION (no reference counterpart; the reference has no prefill MoE path,
- * SURVEY mismatch M6): the routed MoE layer for a chunk of many tokens on the
+ * though the benchmark configuration asks for a 512-token prefill chunk): the
+ * routed MoE layer for a chunk of many tokens on the
  * matrix cores. Same result as mxfp4_moe_grouped_gemv for every token:
  *   out[t] = bf16( sum_k weights[t,k] * W2_e . bf16(silu(W1_e x_t) * (W3_e x_t)) ), e = ids[t,k]
  * with the MXFP4 weights dequantised exactly to bf16 and multiplied on
