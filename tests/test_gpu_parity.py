@@ -572,6 +572,35 @@ def test_moe_prefill_small_vs_oracle(device, T, topk, E):
     assert np.array_equal(host_bits(again), host_bits(out))   # deterministic
 
 
+def test_moe_prefill_special_scale_bytes(device):
+    """E8M0 0xFF (the kernels' zero) and 0 (2^-127, an fp32 subnormal) in some
+    blocks of every matrix: the prefill path must still match the oracle (which
+    keeps byte 0 as 2^-127; the blocks it affects contribute below the
+    tolerance) and the decode path on the same inputs."""
+    E, K, H, O, T, topk = 8, 512, 512, 384, 40, 4
+    announce(f"mxfp4_moe_prefill special scale bytes T={T} topk={topk} E={E}")
+    W1p, W1s = synth.mxfp4_weight(8700, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8704, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8708, O, H, E)
+    rng = np.random.default_rng(8710)
+    for s in (W1s, W3s, W2s):
+        u = rng.random(s.shape)
+        s[u < 0.03] = 0xFF
+        s[(u >= 0.03) & (u < 0.06)] = 0
+    x = synth.normal_bf16(8711, (T, K))
+    ids, w = mx.route_sigmoid_topk(synth.gating_logits(8712, T, E), topk)
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    xd, idd, wd = dev_bf16(x, device), torch.from_numpy(ids).to(device), dev_f32(w, device)
+    out = host_bits(gb.mxfp4_moe_prefill(xd, W1, W3, W2, idd, wd))
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    assert_close(out, mx.moe_layer(x, fn, ids, w, O, n_experts=E), "prefill special scales vs oracle")
+    dec = host_bits(gb.mxfp4_moe_grouped_gemv(xd[:16], W1, W3, W2, idd[:16], wd[:16]))
+    assert_close(out[:16], dec, "prefill special scales vs decode path", cos_tol=0.99999)
+
+
 def test_moe_prefill_config_chunk(device):
     """configs[4] prefill chunk: 512 tokens, top-8 of 256 experts with Zipf
     routing, full dims. Checked token by token against the oracle-checked
