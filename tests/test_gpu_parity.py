@@ -572,6 +572,33 @@ def test_moe_prefill_small_vs_oracle(device, T, topk, E):
     assert np.array_equal(host_bits(again), host_bits(out))   # deterministic
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_special_scale_bytes_decode(device, T):
+    """The decode kernels (one-token and multi-token paths, K = 2048) with E8M0
+    0xFF (decoded as 0) and 0 (2^-127) in some blocks of every matrix, against
+    the oracle's kernel convention."""
+    E, K, H, O, topk = 16, 2048, 256, 384, 8
+    announce(f"mxfp4_moe_grouped_gemv special scale bytes T={T} E={E} K={K}")
+    W1p, W1s = synth.mxfp4_weight(8720, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8724, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8728, O, H, E)
+    rng = np.random.default_rng(8730)
+    for s in (W1s, W3s, W2s):
+        u = rng.random(s.shape)
+        s[u < 0.03] = 0xFF
+        s[(u >= 0.03) & (u < 0.06)] = 0
+    x = synth.normal_bf16(8731 + T, (T, K))
+    ids, w = mx.route_sigmoid_topk(synth.gating_logits(8732 + T, T, E), topk)
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    out = gb.mxfp4_moe_grouped_gemv(dev_bf16(x, device), W1, W3, W2,
+                                    torch.from_numpy(ids).to(device), dev_f32(w, device))
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    assert_close(host_bits(out), mx.moe_layer(x, fn, ids, w, O, n_experts=E), f"special scales T={T}")
+
+
 def test_moe_prefill_special_scale_bytes(device):
     """E8M0 0xFF (the kernels' zero) and 0 (2^-127, an fp32 subnormal) in some
     blocks of every matrix: the prefill path must still match the oracle (which
