@@ -204,60 +204,107 @@ __device__ __forceinline__ float scale_of(uint32_t packed, int j) {
 // maximum: a single such lane holds the pick (its head is the lowest slot
 // among its equal keys); with several (equal logits), a wave min over
 // 64*slot + lane of their heads finds the lowest expert index, on a
-// wave-uniform branch. The winner shifts its list up by one. Only the first
-// `rounds` picks are made. KFIX > 0 bounds the rounds at compile time
-// (rounds <= KFIX), which unrolls them; each unrolled round is skipped by a
-// wave-uniform branch once `rounds` are done.
-template <int KFIX>
-__device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int rounds, int lane, int& me,
-                                                  uint32_t& mk) {
-    uint32_t k[4], s[4];
+// wave-uniform branch. The winner shifts its list up by one. The state can
+// be kept between calls of sorted_heads_rounds, so a wave can stop after the
+// pick it needs and make the rest later.
+struct SortedHeads {
+    uint32_t k[4];   // this lane's remaining keys, largest first (0: none)
+    uint32_t s[4];   // their slots
+    int me;          // lane r < rounds done: index of pick r
+    uint32_t mk;     // lane r < rounds done: key of pick r
+};
+
+__device__ __forceinline__ void sorted_heads_init(const uint32_t (&kv)[4], SortedHeads& h) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        k[i] = kv[i];
-        s[i] = i;
+        h.k[i] = kv[i];
+        h.s[i] = i;
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
 #pragma unroll
         for (int i = p & 1; i + 1 < 4; i += 2) {
-            const bool sw = k[i + 1] > k[i];
-            const uint32_t ka = sw ? k[i + 1] : k[i], kb = sw ? k[i] : k[i + 1];
-            const uint32_t sa = sw ? s[i + 1] : s[i], sb = sw ? s[i] : s[i + 1];
-            k[i] = ka;
-            k[i + 1] = kb;
-            s[i] = sa;
-            s[i + 1] = sb;
+            const bool sw = h.k[i + 1] > h.k[i];
+            const uint32_t ka = sw ? h.k[i + 1] : h.k[i], kb = sw ? h.k[i] : h.k[i + 1];
+            const uint32_t sa = sw ? h.s[i + 1] : h.s[i], sb = sw ? h.s[i] : h.s[i + 1];
+            h.k[i] = ka;
+            h.k[i + 1] = kb;
+            h.s[i] = sa;
+            h.s[i + 1] = sb;
         }
     }
+    h.me = 0;
+    h.mk = 0;
+}
+
+// Rounds r0 .. r1-1 (picks are made in order, so r0 is the number already
+// made). KFIX > 0 bounds r1 at compile time (r1 <= KFIX), which unrolls the
+// rounds; each unrolled round outside [r0, r1) is skipped by a wave-uniform
+// branch.
+template <int KFIX>
+__device__ __forceinline__ void sorted_heads_rounds(SortedHeads& h, int r0, int r1, int lane) {
     auto round = [&](int r) {
-        const uint32_t m = wave_max_u32_uniform(k[0]);
-        const uint64_t b = __ballot(k[0] == m);
+        const uint32_t m = wave_max_u32_uniform(h.k[0]);
+        const uint64_t b = __ballot(h.k[0] == m);
         int idx;
         if (__builtin_popcountll(b) == 1) {
             const int l = __builtin_ctzll(b);
-            idx = 64 * __builtin_amdgcn_readlane(s[0], l) + l;
+            idx = 64 * __builtin_amdgcn_readlane(h.s[0], l) + l;
         } else {
             idx = __builtin_amdgcn_readfirstlane(
-                wave_min_i32(k[0] == m ? (int)(64 * s[0]) + lane : 0x7FFFFFFF));
+                wave_min_i32(h.k[0] == m ? (int)(64 * h.s[0]) + lane : 0x7FFFFFFF));
         }
         const bool hit = lane == (idx & 63);
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            k[i] = hit ? k[i + 1] : k[i];
-            s[i] = hit ? s[i + 1] : s[i];
+            h.k[i] = hit ? h.k[i + 1] : h.k[i];
+            h.s[i] = hit ? h.s[i + 1] : h.s[i];
         }
-        k[3] = hit ? 0u : k[3];
-        me = lane == r ? idx : me;
-        mk = lane == r ? m : mk;
+        h.k[3] = hit ? 0u : h.k[3];
+        h.me = lane == r ? idx : h.me;
+        h.mk = lane == r ? m : h.mk;
     };
     if constexpr (KFIX > 0) {
 #pragma unroll
         for (int r = 0; r < KFIX; ++r)
-            if (r < rounds) round(r);
+            if (r >= r0 && r < r1) round(r);
     } else {
-        for (int r = 0; r < rounds; ++r) round(r);
+        for (int r = r0; r < r1; ++r) round(r);
     }
+}
+
+__device__ __forceinline__ void sorted_heads_rounds_any(SortedHeads& h, int topk, int r0, int r1, int lane) {
+    if (topk == 8) sorted_heads_rounds<8>(h, r0, r1, lane);
+    else sorted_heads_rounds<0>(h, r0, r1, lane);
+}
+
+// Order-preserving keys of one token's logits, PER per lane (expert lane +
+// 64*i): -0 is taken as +0 and NaN as -inf, so equal logits give equal keys;
+// entries past n_experts are key 0, below every logit. The loads are
+// unconditional (index clamped into the row) and all in flight together: the
+// empty asm keeps the compiler from moving a load into the e < n_experts
+// branch, where each would wait for the one before.
+template <int PER>
+__device__ __forceinline__ void logit_keys(const float* lt, int n_experts, int lane, uint32_t (&kv)[PER]) {
+    float lv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) lv[i] = lt[min(lane + 64 * i, n_experts - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(lv[i]));
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const float l = (lv[i] != lv[i]) ? -INFINITY : (lv[i] == 0.f ? 0.f : lv[i]);
+        kv[i] = lane + 64 * i < n_experts ? order_key(l) : 0u;
+    }
+}
+
+// Sigmoid weights of the k picks (lane r < topk holds pick r's key),
+// renormalised to sum 1.
+__device__ __forceinline__ float pick_weights(uint32_t mk, int topk, int lane) {
+    const float my_l = lane < topk ? key_value(mk) : -INFINITY;
+    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
+    return s / wave_sum_f32(s);
 }
 
 // Top-k of one token's logits on one wave: descending, ties to the lower
@@ -266,8 +313,8 @@ __device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int r
 // order-preserving integer keys (larger logit <-> larger key; -0 is taken as
 // +0 and NaN as -inf, so equal logits give equal keys); entries past
 // n_experts and picked entries are key 0, below every logit. With up to 256
-// experts (PER 4) the rounds run on sorted per-lane lists
-// (topk_sorted_heads). Otherwise each round is one integer max reduction over
+// experts (PER 4) the rounds run on sorted per-lane lists (SortedHeads).
+// Otherwise each round is one integer max reduction over
 // every key; the winner's index comes from one ballot per element slot
 // (lowest slot first, then lowest lane: the lowest expert index among equal
 // keys) and is removed by a select.
@@ -277,26 +324,16 @@ __device__ __forceinline__ void topk_sorted_heads(const uint32_t (&kv)[4], int r
 template <int PER>
 __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk, int rounds,
                                                   int lane, int& my_e, float& my_w) {
-    // Unconditional loads (index clamped into the row), all in flight
-    // together: the empty asm keeps the compiler from moving a load into the
-    // e < n_experts branch, where each would wait for the one before.
-    float lv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) lv[i] = lt[min(lane + 64 * i, n_experts - 1)];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(lv[i]));
     uint32_t kv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const float l = (lv[i] != lv[i]) ? -INFINITY : (lv[i] == 0.f ? 0.f : lv[i]);
-        kv[i] = lane + 64 * i < n_experts ? order_key(l) : 0u;
-    }
+    logit_keys<PER>(lt, n_experts, lane, kv);
     int me = 0;
     uint32_t mk = 0;
     if constexpr (PER == 4) {
-        if (topk == 8) topk_sorted_heads<8>(kv, rounds, lane, me, mk);
-        else topk_sorted_heads<0>(kv, rounds, lane, me, mk);
+        SortedHeads h;
+        sorted_heads_init(kv, h);
+        sorted_heads_rounds_any(h, topk, 0, rounds, lane);
+        me = h.me;
+        mk = h.mk;
     } else for (int k = 0; k < rounds; ++k) {
         uint32_t best = kv[0];
 #pragma unroll
@@ -317,12 +354,7 @@ __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts
         mk = lane == k ? m : mk;
     }
     my_e = me;
-    my_w = 0.f;
-    if (rounds == topk) {
-        const float my_l = lane < topk ? key_value(mk) : -INFINITY;
-        const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
-        my_w = s / wave_sum_f32(s);
-    }
+    my_w = rounds == topk ? pick_weights(mk, topk, lane) : 0.f;
 }
 
 __device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int rounds,
@@ -359,6 +391,26 @@ struct GateArgs {
     float* w_out;               // [topk] or null
     RouteTables rt;
 };
+
+// The one-token routing that stage B and the caller read: pick r (lane r <
+// topk) is slot r with pair r, token 0 and its weight.
+__device__ __forceinline__ void publish_routing(const GateArgs& g, int e, float w, int lane) {
+    if (lane < g.topk) {
+        if (g.ids_out != nullptr) {
+            g.ids_out[lane] = e;
+            g.w_out[lane] = w;
+        }
+        g.rt.uexp[lane] = e;
+        g.rt.off[lane] = lane;
+        g.rt.pair_tok[lane] = 0;
+        g.rt.pair_w[lane] = w;
+        if (lane == 0) {
+            g.rt.header[0] = g.topk;
+            g.rt.header[1] = g.topk;
+            g.rt.off[g.topk] = g.topk;
+        }
+    }
+}
 
 struct StageAArgs {
     const uint16_t* x;          // [T, K] bf16
@@ -592,6 +644,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
 
     int expert, pbeg;
     bool valid;
+    SortedHeads heads;   // GATE == 1, up to 256 experts: the ranking state
     if constexpr (GATE == 2) {
         // Wave 0 forms the slots the routing kernel would (the same
         // computation in every workgroup): the distinct in-range ids in
@@ -647,25 +700,22 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         // weight loads; each stops after pick blockIdx.y, the one its
         // workgroup serves. Wave 0 of workgroup (0, 0) ranks all k and
         // publishes the routing for stage B and the caller.
+        // With up to 256 experts the publishing wave, too, first makes only
+        // the pick it serves and finishes the ranking once its weight loads
+        // are in flight (below).
         const GateArgs& g = a.gate;
         const bool publish = blockIdx.x == 0 && blockIdx.y == 0 && wave == 0;
         int e;
-        float w;
-        wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e, w);
-        if (publish && lane < g.topk) {
-            if (g.ids_out != nullptr) {
-                g.ids_out[lane] = e;
-                g.w_out[lane] = w;
-            }
-            g.rt.uexp[lane] = e;
-            g.rt.off[lane] = lane;
-            g.rt.pair_tok[lane] = 0;
-            g.rt.pair_w[lane] = w;
-            if (lane == 0) {
-                g.rt.header[0] = g.topk;
-                g.rt.header[1] = g.topk;
-                g.rt.off[g.topk] = g.topk;
-            }
+        if (g.n_experts <= 256) {
+            uint32_t kv[4];
+            logit_keys<4>(g.logits, g.n_experts, lane, kv);
+            sorted_heads_init(kv, heads);
+            sorted_heads_rounds_any(heads, g.topk, 0, (int)blockIdx.y + 1, lane);
+            e = heads.me;
+        } else {
+            float w;
+            wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e, w);
+            if (publish) publish_routing(g, e, w, lane);
         }
         expert = __builtin_amdgcn_readlane(e, (int)blockIdx.y);
         pbeg = blockIdx.y;
@@ -702,6 +752,18 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     // right after row r is reduced.
 #pragma unroll
     for (int r = 0; r < D; ++r) load_row(r);
+    if constexpr (GATE == 1) {
+        // The publishing wave ranks the remaining picks while its rows are in
+        // flight (keys and lists are in registers: no new load, so nothing
+        // here waits for a row).
+        const GateArgs& g = a.gate;
+        if (g.n_experts <= 256 && blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            sorted_heads_rounds_any(heads, g.topk, 1, g.topk, lane);
+            publish_routing(g, heads.me, pick_weights(heads.mk, g.topk, lane), lane);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 #pragma unroll
     for (int i = 0; i < kXPer; ++i) {
         const int idx = threadIdx.x + kThreads * i;
