@@ -278,6 +278,42 @@ __device__ __forceinline__ void sorted_heads_rounds_any(SortedHeads& h, int topk
     else sorted_heads_rounds<0>(h, r0, r1, lane);
 }
 
+// Expert index of pick y (0-based; the (y+1)-th largest key, equal keys in
+// ascending expert index) by bisection on the key bits: 32 steps, each
+// counting the keys at or above a candidate with one ballot per slot. Its
+// latency does not grow with y, unlike y + 1 selection rounds; the keys are
+// the unsorted ones (slot i of lane l is expert l + 64*i).
+__device__ __forceinline__ int pick_by_bisection(const uint32_t (&kv)[4], int y) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = v | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cnt += __builtin_popcountll(__ballot(kv[i] >= c));
+        v = cnt > y ? c : v;
+    }
+    // v is pick y's key; n of the keys equal to v precede it in index order.
+    int n = y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n -= __builtin_popcountll(__ballot(kv[i] > v));
+    int idx = 0;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint64_t b = __ballot(kv[i] == v);
+        const int c = __builtin_popcountll(b);
+        if (!found && n < c) {
+            for (int j = 0; j < n; ++j) b &= b - 1;
+            idx = 64 * i + __builtin_ctzll(b);
+            found = true;
+        } else if (!found) {
+            n -= c;
+        }
+    }
+    return idx;
+}
+
 // Order-preserving keys of one token's logits, PER per lane (expert lane +
 // 64*i): -0 is taken as +0 and NaN as -inf, so equal logits give equal keys;
 // entries past n_experts are key 0, below every logit. The loads are
@@ -709,9 +745,16 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         if (g.n_experts <= 256) {
             uint32_t kv[4];
             logit_keys<4>(g.logits, g.n_experts, lane, kv);
-            sorted_heads_init(kv, heads);
-            sorted_heads_rounds_any(heads, g.topk, 0, (int)blockIdx.y + 1, lane);
-            e = heads.me;
+            if (blockIdx.y < 4 || publish) {
+                sorted_heads_init(kv, heads);
+                sorted_heads_rounds_any(heads, g.topk, 0, (int)blockIdx.y + 1, lane);
+                e = heads.me;
+            } else {
+                // later picks: bisection, whose latency does not grow with y
+                // (wave-wide ballots: called by every lane; the result is
+                // wave-uniform)
+                e = pick_by_bisection(kv, (int)blockIdx.y);
+            }
         } else {
             float w;
             wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e, w);
