@@ -321,6 +321,16 @@ __device__ __forceinline__ int pick_by_bisection(const uint32_t (&kv)[4], int y)
 // empty asm keeps the compiler from moving a load into the e < n_experts
 // branch, where each would wait for the one before.
 template <int PER>
+__device__ __forceinline__ void keys_of_logits(const float (&lv)[PER], int n_experts, int lane,
+                                               uint32_t (&kv)[PER]) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const float l = (lv[i] != lv[i]) ? -INFINITY : (lv[i] == 0.f ? 0.f : lv[i]);
+        kv[i] = lane + 64 * i < n_experts ? order_key(l) : 0u;
+    }
+}
+
+template <int PER>
 __device__ __forceinline__ void logit_keys(const float* lt, int n_experts, int lane, uint32_t (&kv)[PER]) {
     float lv[PER];
 #pragma unroll
@@ -328,11 +338,7 @@ __device__ __forceinline__ void logit_keys(const float* lt, int n_experts, int l
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(lv[i]));
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const float l = (lv[i] != lv[i]) ? -INFINITY : (lv[i] == 0.f ? 0.f : lv[i]);
-        kv[i] = lane + 64 * i < n_experts ? order_key(l) : 0u;
-    }
+    keys_of_logits<PER>(lv, n_experts, lane, kv);
 }
 
 // Sigmoid weights of the k picks (lane r < topk holds pick r's key),
@@ -673,6 +679,13 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);  // token 0
     const int nx = K / 8;
     const int ns = kRows * nblk / 16;                        // 16-byte scale pieces per matrix
+    // Gated: the first 256 logits are loaded before the activation, so that
+    // the ranking waits for them alone (loads complete in issue order).
+    float lg[GATE == 1 ? 4 : 1];
+    if constexpr (GATE == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lg[i] = a.gate.logits[min(lane + 64 * i, a.gate.n_experts - 1)];
+    }
     u32x4 xv[kXPer];
 #pragma unroll
     for (int i = 0; i < kXPer; ++i) xv[i] = xg[min((int)threadIdx.x + kThreads * i, nx - 1)];
@@ -744,7 +757,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         int e;
         if (g.n_experts <= 256) {
             uint32_t kv[4];
-            logit_keys<4>(g.logits, g.n_experts, lane, kv);
+            keys_of_logits<4>(lg, g.n_experts, lane, kv);
             if (blockIdx.y < 4 || publish) {
                 sorted_heads_init(kv, heads);
                 sorted_heads_rounds_any(heads, g.topk, 0, (int)blockIdx.y + 1, lane);
