@@ -744,14 +744,15 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         pbeg = blockIdx.y;
         valid = (int)blockIdx.y < s_nu[0];
     } else if constexpr (GATE == 1) {
-        // Every wave ranks the logits itself (the same computation in every
-        // wave of every workgroup), so no wave waits on another before its
-        // weight loads; each stops after pick blockIdx.y, the one its
-        // workgroup serves. Wave 0 of workgroup (0, 0) ranks all k and
-        // publishes the routing for stage B and the caller.
-        // With up to 256 experts the publishing wave, too, first makes only
-        // the pick it serves and finishes the ranking once its weight loads
-        // are in flight (below).
+        // Every wave ranks the logits itself, so no wave waits on another
+        // before its weight loads, and it stops at pick blockIdx.y, the one
+        // its workgroup serves: with up to 256 experts, slots 0-3 by selection
+        // rounds on sorted per-lane lists and later slots by bisection, whose
+        // latency does not grow with the slot. Wave 0 of workgroup (0, 0)
+        // publishes the routing for stage B and the caller: with up to 256
+        // experts it makes its own pick first and finishes the ranking once
+        // its weight loads are in flight (below); with more it ranks all k
+        // first.
         const GateArgs& g = a.gate;
         const bool publish = blockIdx.x == 0 && blockIdx.y == 0 && wave == 0;
         int e;
@@ -763,9 +764,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
                 sorted_heads_rounds_any(heads, g.topk, 0, (int)blockIdx.y + 1, lane);
                 e = heads.me;
             } else {
-                // later picks: bisection, whose latency does not grow with y
-                // (wave-wide ballots: called by every lane; the result is
-                // wave-uniform)
+                // wave-wide ballots: called by every lane, wave-uniform result
                 e = pick_by_bisection(kv, (int)blockIdx.y);
             }
         } else {
