@@ -679,12 +679,19 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
     const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);  // token 0
     const int nx = K / 8;
     const int ns = kRows * nblk / 16;                        // 16-byte scale pieces per matrix
-    // Gated: the first 256 logits are loaded before the activation, so that
-    // the ranking waits for them alone (loads complete in issue order).
+    // Gated: the first 256 logits (ids given: the ids and weights) are
+    // loaded before the activation, so that the routing waits for them alone
+    // (loads complete in issue order).
     float lg[GATE == 1 ? 4 : 1];
+    int id_l = 0;
+    float idw_l = 0.f;
     if constexpr (GATE == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) lg[i] = a.gate.logits[min(lane + 64 * i, a.gate.n_experts - 1)];
+    } else if constexpr (GATE == 2) {
+        const int k = min(lane, a.gate.topk - 1);
+        id_l = a.gate.ids_in[k];
+        idw_l = a.gate.w_in[k];
     }
     u32x4 xv[kXPer];
 #pragma unroll
@@ -701,9 +708,8 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         // listing order). Workgroup (0, 0) publishes them for stage B.
         if (wave == 0) {
             const GateArgs& g = a.gate;
-            const int k = min(lane, g.topk - 1);
-            const int e = g.ids_in[k];
-            const float wl = g.w_in[k];
+            const int e = id_l;
+            const float wl = idw_l;
             const bool listed = lane < g.topk;
             bool first = true;
             float wsum = 0.f;
