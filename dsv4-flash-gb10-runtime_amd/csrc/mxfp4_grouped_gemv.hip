@@ -32,7 +32,6 @@
 //     tables, each unique expert streamed once for all of its tokens).
 
 #include <cstdio>
-#include <cstdlib>
 #include <cstring>
 
 #include "dsv4_device.h"
@@ -48,6 +47,7 @@ constexpr int kMaxExpSlots = 256;       // n_exp cap of the drop-in entry
 constexpr int kMaxTokens = 64;          // T cap of the expert-indexed entry
 constexpr int kMaxTopk = 16;
 constexpr int kMaxExperts = 1024;
+constexpr int kMaxRouterK = 8192;       // router gate row length cap (16 KiB of bf16 per row)
 
 constexpr int kWavesA = 4;              // waves per stage-A workgroup
 
@@ -314,43 +314,75 @@ __device__ __forceinline__ int pick_by_bisection(const uint32_t (&kv)[4], int y)
     return idx;
 }
 
-// Order-preserving keys of one token's logits, PER per lane (expert lane +
-// 64*i): -0 is taken as +0 and NaN as -inf, so equal logits give equal keys;
-// entries past n_experts are key 0, below every logit. The loads are
-// unconditional (index clamped into the row) and all in flight together: the
-// empty asm keeps the compiler from moving a load into the e < n_experts
-// branch, where each would wait for the one before.
+// How the picks are scored and weighted:
+//   kScoreSigmoid (the benchmark configuration): rank the logits; weight
+//     w_k = sigmoid(l_k) / sum_k' sigmoid(l_k');
+//   kScoreSqrtSoftplus (the reference engine's router,
+//     kernel/cpp-engine-mxfp4/routed.cu:156-208): rank the scores
+//     s = sqrt(softplus(l)), softplus(l) = max(l, 0) + log1p(exp(-|l|));
+//     weight w_k = (s_k / (sum_k' s_k' + 1e-20f)) * scale, evaluated in double
+//     with the sum taken in pick order, then rounded to float, as the
+//     reference's host code does.
+// Ranking is by value, descending, ties to the lower expert index. A NaN
+// logit or score ranks below every number (the reference never picks one;
+// with fewer than k numbers it aborts, here the NaN entries fill the picks).
+enum ScoreMode : int { kScoreSigmoid = 0, kScoreSqrtSoftplus = 1 };
+
+struct Scoring {
+    int mode;
+    float scale;            // kScoreSqrtSoftplus: the routed scaling factor
+};
+
+__device__ __forceinline__ float sqrt_softplus(float l) {
+    return sqrtf(fmaxf(l, 0.f) + log1pf(expf(-fabsf(l))));
+}
+
+// Order-preserving keys of one token's scores, PER per lane (expert lane +
+// 64*i): -0 is taken as +0 and NaN as -inf, so equal values give equal keys;
+// entries past n_experts are key 0, below every value.
 template <int PER>
 __device__ __forceinline__ void keys_of_logits(const float (&lv)[PER], int n_experts, int lane,
-                                               uint32_t (&kv)[PER]) {
+                                               const Scoring& sc, uint32_t (&kv)[PER]) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const float l = (lv[i] != lv[i]) ? -INFINITY : (lv[i] == 0.f ? 0.f : lv[i]);
+        const float v = sc.mode == kScoreSqrtSoftplus ? sqrt_softplus(lv[i]) : lv[i];
+        const float l = (v != v) ? -INFINITY : (v == 0.f ? 0.f : v);
         kv[i] = lane + 64 * i < n_experts ? order_key(l) : 0u;
     }
 }
 
+// The loads are unconditional (index clamped into the row) and all in flight
+// together: the empty asm keeps the compiler from moving a load into the
+// e < n_experts branch, where each would wait for the one before.
 template <int PER>
-__device__ __forceinline__ void logit_keys(const float* lt, int n_experts, int lane, uint32_t (&kv)[PER]) {
+__device__ __forceinline__ void logit_keys(const float* lt, int n_experts, int lane, const Scoring& sc,
+                                           uint32_t (&kv)[PER]) {
     float lv[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) lv[i] = lt[min(lane + 64 * i, n_experts - 1)];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(lv[i]));
-    keys_of_logits<PER>(lv, n_experts, lane, kv);
+    keys_of_logits<PER>(lv, n_experts, lane, sc, kv);
 }
 
-// Sigmoid weights of the k picks (lane r < topk holds pick r's key),
-// renormalised to sum 1.
-__device__ __forceinline__ float pick_weights(uint32_t mk, int topk, int lane) {
-    const float my_l = lane < topk ? key_value(mk) : -INFINITY;
-    const float s = lane < topk ? 1.0f / (1.0f + __expf(-my_l)) : 0.f;
+// Weights of the k picks (lane r < topk holds pick r's key; the result is
+// for lane r's pick, 0 on lanes >= topk).
+__device__ __forceinline__ float pick_weights(uint32_t mk, int topk, int lane, const Scoring& sc) {
+    const float v = lane < topk ? key_value(mk) : 0.f;
+    if (sc.mode == kScoreSqrtSoftplus) {
+        double sum = 0.0;
+        for (int k = 0; k < topk; ++k)
+            sum += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), k));
+        const double denom = sum + (double)1e-20f;
+        return lane < topk ? (float)(((double)v / denom) * (double)sc.scale) : 0.f;
+    }
+    const float s = lane < topk ? 1.0f / (1.0f + __expf(-v)) : 0.f;
     return s / wave_sum_f32(s);
 }
 
 // Top-k of one token's logits on one wave: descending, ties to the lower
-// expert index, weights sigmoid(l) renormalised to sum 1. Lane k < topk
+// expert index, weights as `sc` says (Scoring). Lane k < topk
 // returns the k-th pick. Each lane holds PER logits (expert lane + 64*i) as
 // order-preserving integer keys (larger logit <-> larger key; -0 is taken as
 // +0 and NaN as -inf, so equal logits give equal keys); entries past
@@ -364,10 +396,10 @@ __device__ __forceinline__ float pick_weights(uint32_t mk, int topk, int lane) {
 // at or past it return expert 0. The weights need every pick, so they are
 // computed only when rounds == topk (my_w is 0 otherwise).
 template <int PER>
-__device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts, int topk, int rounds,
-                                                  int lane, int& my_e, float& my_w) {
+__device__ __forceinline__ void wave_topk(const float* lt, int n_experts, int topk, int rounds,
+                                          const Scoring& sc, int lane, int& my_e, float& my_w) {
     uint32_t kv[PER];
-    logit_keys<PER>(lt, n_experts, lane, kv);
+    logit_keys<PER>(lt, n_experts, lane, sc, kv);
     int me = 0;
     uint32_t mk = 0;
     if constexpr (PER == 4) {
@@ -396,14 +428,14 @@ __device__ __forceinline__ void wave_topk_sigmoid(const float* lt, int n_experts
         mk = lane == k ? m : mk;
     }
     my_e = me;
-    my_w = rounds == topk ? pick_weights(mk, topk, lane) : 0.f;
+    my_w = rounds == topk ? pick_weights(mk, topk, lane, sc) : 0.f;
 }
 
 __device__ __forceinline__ void wave_topk_any(const float* lt, int n_experts, int topk, int rounds,
-                                              int lane, int& e, float& w) {
-    if (n_experts <= 256) wave_topk_sigmoid<4>(lt, n_experts, topk, rounds, lane, e, w);
-    else if (n_experts <= 512) wave_topk_sigmoid<8>(lt, n_experts, topk, rounds, lane, e, w);
-    else wave_topk_sigmoid<16>(lt, n_experts, topk, rounds, lane, e, w);
+                                              const Scoring& sc, int lane, int& e, float& w) {
+    if (n_experts <= 256) wave_topk<4>(lt, n_experts, topk, rounds, sc, lane, e, w);
+    else if (n_experts <= 512) wave_topk<8>(lt, n_experts, topk, rounds, sc, lane, e, w);
+    else wave_topk<16>(lt, n_experts, topk, rounds, sc, lane, e, w);
 }
 
 // ---------------------------------------------------------------- stage A --
@@ -432,16 +464,15 @@ struct GateArgs {
     int32_t* ids_out;           // [topk] or null (logits only)
     float* w_out;               // [topk] or null
     RouteTables rt;
+    Scoring sc;                 // logits only: scoring and weights of the picks
 };
 
 // The one-token routing that stage B and the caller read: pick r (lane r <
 // topk) is slot r with pair r, token 0 and its weight.
 __device__ __forceinline__ void publish_routing(const GateArgs& g, int e, float w, int lane) {
     if (lane < g.topk) {
-        if (g.ids_out != nullptr) {
-            g.ids_out[lane] = e;
-            g.w_out[lane] = w;
-        }
+        if (g.ids_out != nullptr) g.ids_out[lane] = e;
+        if (g.w_out != nullptr) g.w_out[lane] = w;
         g.rt.uexp[lane] = e;
         g.rt.off[lane] = lane;
         g.rt.pair_tok[lane] = 0;
@@ -464,7 +495,6 @@ struct StageAArgs {
     int64_t s_exp_stride;       // bytes per expert: hidden * K/32
     int K;
     int hidden;
-    int h_per_wave;             // multiple of the chunk height
     int scale_vec;              // scale rows allow NB-byte vector loads
     uint16_t* M;                // [pairs, hidden] bf16
     ExpertSet es;
@@ -484,22 +514,21 @@ struct GateUpChunk {
     uint32_t s3[HC];
 };
 
-// grid = (ceil(hidden / (kWavesA*h_per_wave)), expert slots), block = 64*kWavesA.
-// Each wave walks its hidden rows in chunks of HC with two register buffers:
-// the loads of chunk c+1 are in flight while chunk c is reduced. On the FAST
-// path every load is unconditional (a prefetch past the wave's last chunk
-// re-reads the current one, which hits in cache), so the compiler can wait on
-// exactly the loads a chunk needs rather than draining the prefetch.
-template <int NB, int HC, bool INDEXED, bool FAST, bool PIPE, bool MULTI>
-__global__ __launch_bounds__(64 * kWavesA, PIPE ? 1 : 4) void moe_swiglu_kernel(const StageAArgs a) {
+// grid = (ceil(hidden / (kWavesA*HC)), expert slots), block = 64*kWavesA.
+// Each wave owns one chunk of HC hidden rows; occupancy, not a loop,
+// overlaps the loads of different waves. On the FAST path every load is
+// unconditional (rows past the end are clamped to the last row, loaded and
+// never stored), so the compiler waits on exactly the loads a step needs.
+template <int NB, int HC, bool INDEXED, bool FAST, bool MULTI>
+__global__ __launch_bounds__(64 * kWavesA, 4) void moe_swiglu_kernel(const StageAArgs a) {
     constexpr bool ALIGNED = FAST;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     int expert, pbeg, pend;
     if (!slot_info<INDEXED>(a.es, blockIdx.y, expert, pbeg, pend)) return;
-    const int h_begin = (blockIdx.x * kWavesA + wave) * a.h_per_wave;
+    const int h_begin = (blockIdx.x * kWavesA + wave) * HC;
     if (h_begin >= a.hidden) return;
-    const int h_end = min(h_begin + a.h_per_wave, a.hidden);
+    const int h_end = min(h_begin + HC, a.hidden);
 
     const int K = a.K;
     const int nblk = K / kBlkElems;
@@ -588,58 +617,29 @@ __global__ __launch_bounds__(64 * kWavesA, PIPE ? 1 : 4) void moe_swiglu_kernel(
             a.M[(int64_t)p * a.hidden + h0 + r] = f32_to_bf16_bits(silu_f32(g[0]) * u[0]);
     };
 
-    GateUpChunk<NB, HC> ca, cb;
-    if (!MULTI || pend - pbeg == 1) {
-        // One (token, weight) pair: the activation stays in registers and the
-        // chunks stream through a two-deep pipeline.
-        int tok;
-        float wt;
-        pair_info<INDEXED>(a.es, pbeg, tok, wt);
-        load_x(tok);
-        load_chunk(h_begin, ca);
-        if constexpr (!PIPE) {
-            // One chunk per wave (h_per_wave == HC): occupancy, not a loop,
-            // overlaps the loads of different waves.
-            emit(ca, h_begin, pbeg);
-            return;
-        }
-        int h0 = h_begin;
-        while (true) {
-            const int hn = h0 + HC < h_end ? h0 + HC : h0;
-            if constexpr (FAST) load_chunk(hn, cb);
-            else if (hn != h0) load_chunk(hn, cb);
-            emit(ca, h0, pbeg);
-            h0 += HC;
-            if (h0 >= h_end) break;
-            const int hm = h0 + HC < h_end ? h0 + HC : h0;
-            if constexpr (FAST) load_chunk(hm, ca);
-            else if (hm != h0) load_chunk(hm, ca);
-            emit(cb, h0, pbeg);
-            h0 += HC;
-            if (h0 >= h_end) break;
-        }
-    } else if constexpr (MULTI) {
-        // Several tokens share this expert: each chunk is loaded once and
-        // reduced against every token's activation.
+    int tok;
+    float wt;
+    pair_info<INDEXED>(a.es, pbeg, tok, wt);
+    load_x(tok);
+    GateUpChunk<NB, HC> ca;
+    load_chunk(h_begin, ca);
+    emit(ca, h_begin, pbeg);
+    if constexpr (MULTI) {
+        // Further tokens of this expert: the chunk stays in registers and is
+        // reduced against each token's activation.
 #pragma unroll 1
-        for (int h0 = h_begin; h0 < h_end; h0 += HC) {
-            load_chunk(h0, ca);
-#pragma unroll 1
-            for (int p = pbeg; p < pend; ++p) {
-                int tok;
-                float wt;
-                pair_info<INDEXED>(a.es, p, tok, wt);
-                load_x(tok);
+        for (int p = pbeg + 1; p < pend; ++p) {
+            pair_info<INDEXED>(a.es, p, tok, wt);
+            load_x(tok);
 #pragma unroll
-                for (int r = 0; r < HC; ++r) {
+            for (int r = 0; r < HC; ++r) {
 #pragma unroll
-                    for (int j = 0; j < NB; ++j) {
-                        reg_barrier(ca.w1[r][j]);
-                        reg_barrier(ca.w3[r][j]);
-                    }
+                for (int j = 0; j < NB; ++j) {
+                    reg_barrier(ca.w1[r][j]);
+                    reg_barrier(ca.w3[r][j]);
                 }
-                emit(ca, h0, p);
             }
+            emit(ca, h_begin, p);
         }
     }
 }
@@ -764,7 +764,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         int e;
         if (g.n_experts <= 256) {
             uint32_t kv[4];
-            keys_of_logits<4>(lg, g.n_experts, lane, kv);
+            keys_of_logits<4>(lg, g.n_experts, lane, g.sc, kv);
             if (blockIdx.y < 4 || publish) {
                 sorted_heads_init(kv, heads);
                 sorted_heads_rounds_any(heads, g.topk, 0, (int)blockIdx.y + 1, lane);
@@ -775,7 +775,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
             }
         } else {
             float w;
-            wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, lane, e, w);
+            wave_topk_any(g.logits, g.n_experts, g.topk, publish ? g.topk : (int)blockIdx.y + 1, g.sc, lane, e, w);
             if (publish) publish_routing(g, e, w, lane);
         }
         expert = __builtin_amdgcn_readlane(e, (int)blockIdx.y);
@@ -821,7 +821,7 @@ __global__ __launch_bounds__(64 * kT1Waves, 4) void moe_swiglu_t1_kernel(const S
         if (g.n_experts <= 256 && blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
             __builtin_amdgcn_sched_barrier(0);
             sorted_heads_rounds_any(heads, g.topk, 1, g.topk, lane);
-            publish_routing(g, heads.me, pick_weights(heads.mk, g.topk, lane), lane);
+            publish_routing(g, heads.me, pick_weights(heads.mk, g.topk, lane, g.sc), lane);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -1066,7 +1066,6 @@ struct StageBArgs {
     int out_dim;
     int T;
     int scale_vec;
-    int stage_scales;           // one-token path: scale rows staged per wave (out_dim % 8 == 0, 16-byte aligned)
     uint16_t* out;              // [T, out_dim] bf16
     ExpertSet es;
 };
@@ -1088,25 +1087,21 @@ struct DownRows {
 };
 
 // grid = ceil(out_dim / kRowsB), block = 64*kWavesB. Wave w takes expert
-// slots w, w+kWavesB, ... for the workgroup's kRowsB output rows, with the
-// next slot's rows loading while the current one is reduced (on the FAST path
-// the prefetch is unconditional: past the last slot it re-reads the current
-// rows); partial sums per (wave, token, row) meet in LDS and are added in wave
-// order.
-template <int NBB, int RB, int WB, int TMAX, bool INDEXED, bool FAST, bool PIPE, bool MULTI, int BD = RB>
-__global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_down_kernel(const StageBArgs a) {
+// slots w, w+kWavesB, ... for the workgroup's kRowsB output rows; partial sums
+// per (wave, token, row) meet in LDS and are added in wave order. This is the
+// general kernel: the one-token and multi-token kernels below cover the
+// aligned config shapes; it serves the rest (other hidden sizes, unaligned
+// operands, one token with more than 8 routed slots).
+template <int NBB, int RB, int WB, int TMAX, bool INDEXED, bool FAST, bool MULTI>
+__global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_kernel(const StageBArgs a) {
     constexpr bool ALIGNED = FAST;
     constexpr int kRowsB = RB;
     constexpr int kWavesB = WB;
     __shared__ float acc[kWavesB][TMAX][kRowsB];
-    __shared__ __align__(16) uint8_t sstage[(!PIPE && !MULTI && FAST) ? kWavesB : 1][kRowsB * 64 * NBB];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar table loads
     const int o0 = blockIdx.x * kRowsB;
-    // The one-token path writes every acc[wave][0][r] itself; the others
-    // accumulate into zeroed slots.
-    const bool t1_path = !PIPE && !MULTI && FAST && a.stage_scales && a.es.n_slots <= kWavesB;
-    if (!t1_path) {
+    {
         float* accf = &acc[0][0][0];
         for (int i = threadIdx.x; i < kWavesB * TMAX * kRowsB; i += 64 * kWavesB) accf[i] = 0.f;
         __syncthreads();
@@ -1192,90 +1187,11 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
         }
     };
 
-    DownRows<NBB, RB> da, db;
-    int u = wave;
-    if (t1_path) {
-        // One token (host-checked: at most one slot per wave, whole 16-row
-        // tiles, 16-byte aligned scales). Wave w takes slot w: its table
-        // reads are unconditional (slot_info_t1); its M slice, then its
-        // kRowsB scale rows (one load of kRowsB*NBB bytes per lane, spread
-        // through the wave's LDS slot), then its W2 rows are issued, so the
-        // dots start as soon as the first row arrives. No branch surrounds a
-        // load, so every wait covers exactly the loads it needs.
-        int expert, pbeg;
-        float wt;
-        bool valid;
-        slot_info_t1_wave<INDEXED>(a.es, wave, lane, expert, pbeg, wt, valid);
-        uint32_t ms[NBB][16];
-#pragma unroll
-        for (int j = 0; j < NBB; ++j)
-            load_act_block<true>(a.M + (int64_t)pbeg * a.hidden + (b0 + j) * kBlkElems, ms[j]);
-        const uint8_t* W2 = a.w2 + (int64_t)expert * a.w_exp_stride;
-        const uint8_t* S2 = a.s2 + (int64_t)expert * a.s_exp_stride;
-        using SPiece = typename ScalePiece<kRowsB * NBB>::type;
-        const SPiece spiece =
-            *reinterpret_cast<const SPiece*>(S2 + (int64_t)o0 * nblk + lane * (kRowsB * NBB));
-        __builtin_amdgcn_sched_barrier(0);  // keep the M and scale loads oldest
-        auto load_row = [&](int r) {
-            const int o = min(o0 + r, a.out_dim - 1);
-#pragma unroll
-            for (int j = 0; j < NBB; ++j)
-                da.w[r][j] = ld16_stream(W2 + (int64_t)o * wrow + (int64_t)(b0 + j) * 16);
-        };
-#pragma unroll
-        for (int r = 0; r < BD; ++r) load_row(r);
-        reinterpret_cast<SPiece*>(&sstage[wave][0])[lane] = spiece;
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int r = 0; r < kRowsB; ++r) {
-            uint32_t v = 0;
-#pragma unroll
-            for (int j = 0; j < NBB; ++j) v |= (uint32_t)sstage[wave][r * nblk + b0 + j] << (8 * j);
-            da.s[r] = v;
-        }
-        float part[kRowsB];
-        float chain = 0.f;
-#pragma unroll
-        for (int r = 0; r < kRowsB; ++r) {
-            float sum = 0.f;
-#pragma unroll
-            for (int j = 0; j < NBB; ++j) {
-                reg_barrier_after(da.w[r][j], chain);
-                sum = fmaf(fp4_block_dot(da.w[r][j], ms[j]), scale_of(da.s[r], j), sum);
-                chain = sum;
-            }
-            part[r] = sum;
-            if (r + BD < kRowsB) {
-                __builtin_amdgcn_sched_barrier(0);
-                load_row(r + BD);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        wave_reduce_n<kRowsB>(part, lane);
-        const int r = reduced_index<kRowsB>(lane);
-        if (reduced_owner<kRowsB>(lane)) acc[wave][0][r] = valid ? wt * part[0] : 0.f;  // out_dim % 16 == 0
-    } else if (!PIPE) {
+    DownRows<NBB, RB> da;
 #pragma unroll 1
-        for (; u < U; u += kWavesB) {
-            load_rows(u, da);
-            process(da, u);
-        }
-    } else if (u < U) {
+    for (int u = wave; u < U; u += kWavesB) {
         load_rows(u, da);
-        while (true) {
-            const int un = u + kWavesB < U ? u + kWavesB : u;
-            if constexpr (FAST) load_rows(un, db);
-            else if (un != u) load_rows(un, db);
-            process(da, u);
-            u += kWavesB;
-            if (u >= U) break;
-            const int um = u + kWavesB < U ? u + kWavesB : u;
-            if constexpr (FAST) load_rows(um, da);
-            else if (um != u) load_rows(um, da);
-            process(db, u);
-            u += kWavesB;
-            if (u >= U) break;
-        }
+        process(da, u);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < a.T * kRowsB; i += 64 * kWavesB) {
@@ -1300,7 +1216,7 @@ __global__ __launch_bounds__(64 * WB, PIPE ? 1 : (WB >= 8 ? 2 : 4)) void moe_dow
 // the first row arrives. No branch surrounds a load. Slots past the routed
 // ones load a valid expert's rows and contribute 0. The RB row sums of the
 // WB waves meet in LDS and are added in wave order, then rounded to bf16.
-template <int NBB, int RB, int WB, bool INDEXED, int BD>
+template <int NBB, int RB, int WB, bool INDEXED>
 __global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_t1_kernel(const StageBArgs a) {
     __shared__ float acc[WB][RB];
     __shared__ __align__(16) uint8_t sstage[WB][RB * 64 * NBB];
@@ -1330,7 +1246,7 @@ __global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_t1_kernel(c
             w[r][j] = ld16_stream(W2 + (int64_t)(o0 + r) * wrow + (int64_t)(b0 + j) * 16);
     };
 #pragma unroll
-    for (int r = 0; r < BD; ++r) load_row(r);
+    for (int r = 0; r < RB; ++r) load_row(r);  // every row in flight before the first dot
     reinterpret_cast<SPiece*>(&sstage[wave][0])[lane] = spiece;
     __builtin_amdgcn_wave_barrier();
     uint32_t sc[RB];
@@ -1353,11 +1269,6 @@ __global__ __launch_bounds__(64 * WB, WB >= 8 ? 2 : 4) void moe_down_t1_kernel(c
             chain = sum;
         }
         part[r] = sum;
-        if (r + BD < RB) {
-            __builtin_amdgcn_sched_barrier(0);
-            load_row(r + BD);
-            __builtin_amdgcn_sched_barrier(0);
-        }
     }
     wave_reduce_n<RB>(part, lane);
     const int r = reduced_index<RB>(lane);
@@ -1517,7 +1428,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
                                                                   const int32_t* ids_in,
                                                                   const float* w_in, int T, int topk,
                                                                   int n_experts, int32_t* ids_out,
-                                                                  float* w_out, RouteTables rt) {
+                                                                  float* w_out, RouteTables rt, Scoring sc) {
     __shared__ int cnt[kMaxExperts];
     __shared__ int scan[kRouteThreads / 64];
     __shared__ int sid[kMaxTokens * kMaxTopk];
@@ -1532,7 +1443,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
         for (int t = wave; t < T; t += kRouteThreads / 64) {
             int e;
             float w;
-            wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, topk, lane, e, w);
+            wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, topk, sc, lane, e, w);
             if (lane < topk) {
                 sid[t * topk + lane] = e;
                 sw[t * topk + lane] = w;
@@ -1568,10 +1479,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
             }
             take[q] = first && e >= 0 && e < n_experts;
             wsum[q] = w;
-            if (ids_out != nullptr) {
-                ids_out[i] = e;
-                w_out[i] = sw[i];
-            }
+            if (ids_out != nullptr) ids_out[i] = e;
+            if (w_out != nullptr) w_out[i] = sw[i];
             if (take[q]) atomicAdd(&cnt[e], 1);
         }
     }
@@ -1635,75 +1544,73 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
 }
 
 // Gating only: one wave per token writes ids [T, topk] and weights [T, topk].
-__global__ __launch_bounds__(64) void moe_route_sigmoid_topk_kernel(const float* logits,
-                                                                     int n_experts, int topk,
-                                                                     int32_t* ids, float* wout) {
+__global__ __launch_bounds__(64) void moe_route_topk_kernel(const float* logits, int n_experts, int topk,
+                                                            Scoring sc, int32_t* ids, float* wout) {
     const int t = blockIdx.x;
     const int lane = threadIdx.x;
     int e;
     float w;
-    wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, topk, lane, e, w);
+    wave_topk_any(logits + (int64_t)t * n_experts, n_experts, topk, topk, sc, lane, e, w);
     if (lane < topk) {
         ids[(int64_t)t * topk + lane] = e;
         wout[(int64_t)t * topk + lane] = w;
     }
 }
 
-// ------------------------------------------------------------ host side ----
+// ------------------------------------------------------------ router -----
 
-int env_int(const char* name, int def) {
-    const char* s = std::getenv(name);
-    if (!s || !*s) return def;
-    const int v = std::atoi(s);
-    return v > 0 ? v : def;
+// Router gate GEMV (reference kernel/cpp-engine-mxfp4/routed.cu:124-153):
+//   logits[t, n] = sum_k Wg[n, k] * x[t, k],  bf16 operands, fp32 accumulate.
+// One wave per gate row; lane l owns the 16-byte pieces l, l+64, ... of the
+// row (each load instruction reads one contiguous KiB), which stay in
+// registers while the T tokens' activation pieces (L2 hits after the first
+// wave) are dotted against them with v_dot2_f32_bf16; the lane sums are
+// reduced over the wave. Pieces past the row (K not a multiple of 512) are
+// loaded clamped and multiplied by zero activations.
+constexpr int kRouterWaves = 4;
+
+template <int NJ>
+__global__ __launch_bounds__(64 * kRouterWaves) void moe_router_gemv_kernel(const uint16_t* x, const uint16_t* wg,
+                                                                            int T, int n_rows, int K,
+                                                                            float* logits) {
+    const int lane = threadIdx.x & 63;
+    const int row = min((int)(blockIdx.x * kRouterWaves + (threadIdx.x >> 6)), n_rows - 1);
+    const int npc = K / 8;                     // 16-byte pieces per row
+    const uint16_t* wr = wg + (int64_t)row * K;
+    u32x4 w[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) w[j] = ld16_stream(reinterpret_cast<const uint8_t*>(wr + 8 * min(lane + 64 * j, npc - 1)));
+    for (int t = 0; t < T; ++t) {
+        const uint16_t* xt = x + (int64_t)t * K;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int pc = lane + 64 * j;
+            u32x4 xv = *reinterpret_cast<const u32x4*>(xt + 8 * min(pc, npc - 1));
+            if (pc >= npc) xv = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = dot2(as_bf16x2(w[j][q]), as_bf16x2(xv[q]), acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0 && blockIdx.x * kRouterWaves + (threadIdx.x >> 6) < (unsigned)n_rows)
+            logits[(int64_t)t * n_rows + row] = acc;
+    }
 }
 
-// Launch shapes. Stage A: hidden rows per chunk HC (2 or 4) and whether a
-// wave pipelines several chunks (PIPE, rows per wave from
-// DSV4_GROUPED_H_PER_WAVE) or owns exactly one. Stage B: output rows per
-// workgroup RB, waves per workgroup WB, pipelined expert slots or not.
-// Defaults come from sweeps on MI355X; the environment variables exist for
-// re-tuning (DSV4_GROUPED_HC, DSV4_GROUPED_PIPE, DSV4_GROUPED_H_PER_WAVE,
-// DSV4_GROUPED_B = RB*100 + WB*10 + PIPE, e.g. 880).
-struct Shapes {
-    int hc, pipe, h_per_wave;
-    int rb, wb, bpipe;
-    int t1, t1_waves, b1_depth;
-    int tn;                     // activations staged per pass by the multi-token kernel (0: generic kernel)
-    int tnb;                    // multi-token stage B: pipelined kernel (1) or generic (0)
-};
-
-const Shapes& shapes() {
-    static const Shapes s = [] {
-        Shapes v;
-        v.hc = env_int("DSV4_GROUPED_HC", 4) >= 4 ? 4 : 2;
-        v.pipe = env_int("DSV4_GROUPED_PIPE", 0) == 1 ? 1 : 0;
-        int r = env_int("DSV4_GROUPED_H_PER_WAVE", v.hc * 4);
-        v.h_per_wave = v.pipe ? (r + v.hc - 1) / v.hc * v.hc : v.hc;
-        const int b = env_int("DSV4_GROUPED_B", 880);
-        v.rb = (b / 100) >= 16 ? 16 : 8;
-        v.wb = ((b / 10) % 10) >= 8 ? 8 : 4;
-        v.bpipe = b % 10 == 1;
-        // One-token stage A: DSV4_GROUPED_T1 = waves per workgroup (4, 8, 16;
-        // "0" selects the generic kernel).
-        const int t1 = env_int("DSV4_GROUPED_T1", 4);
-        v.t1 = 1;
-        v.t1_waves = t1 >= 16 ? 16 : (t1 >= 8 ? 8 : 4);
-        if (std::getenv("DSV4_GROUPED_T1") && std::atoi(std::getenv("DSV4_GROUPED_T1")) == 0) v.t1 = 0;
-        // Rows in flight before the first dot of one-token stage B (of 8).
-        v.b1_depth = env_int("DSV4_GROUPED_B1_DEPTH", 8);
-        // Multi-token stage A: DSV4_GROUPED_TN = activations staged per pass
-        // (1 or 2; 0 selects the generic kernel).
-        const char* tn_env = std::getenv("DSV4_GROUPED_TN");
-        const int tn = tn_env ? std::atoi(tn_env) : 2;
-        v.tn = tn >= 2 ? 2 : (tn >= 1 ? 1 : 0);
-        // Multi-token stage B: DSV4_GROUPED_TNB = 0 selects the generic kernel.
-        const char* tnb_env = std::getenv("DSV4_GROUPED_TNB");
-        v.tnb = tnb_env ? (std::atoi(tnb_env) != 0) : 1;
-        return v;
-    }();
-    return s;
-}
+// Launch shapes (fixed; chosen by sweeps on MI355X):
+//   stage A, one token: moe_swiglu_t1_kernel with 4 waves of 4 rows each per
+//     workgroup (16 hidden rows of one expert slot);
+//   stage A, several tokens: moe_swiglu_tn_kernel, 16 rows per workgroup,
+//     two further activations staged per pass;
+//   stage A otherwise: moe_swiglu_kernel, one chunk of 4 rows (2 on the
+//     checked path) per wave;
+//   stage B: 8 output rows per workgroup of 8 waves (one-token, multi-token
+//     and general kernels alike).
+constexpr int kT1Waves = 4;
+constexpr int kChunkFast = 4;
+constexpr int kChunkChecked = 2;
+constexpr int kRowsDown = 8;
+constexpr int kWavesDown = 8;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -1720,76 +1627,60 @@ int scale_vec_ok(int nb, int nblk, const void* s0, const void* s1) {
 
 // FAST kernels: 16-byte aligned operands, every lane owning NB whole blocks of
 // every row (K == 2048*NB) and NB-byte scale loads; other shapes take the
-// checked path (HC = 2, one chunk per wave).
+// checked path (HC = 2).
 //
 // Whether stage A of a one-token launch takes moe_swiglu_t1_kernel (16-byte
-// aligned operands, K = 2048 or 4096, whole row tiles, aligned scale rows).
+// aligned operands, K = 2048 or 4096, whole 16-row tiles, aligned scale rows).
 bool stage_a_t1_ok(const StageAArgs& a, bool aligned) {
-    const Shapes& sh = shapes();
     const int nb = blocks_per_lane(a.K);
     const bool fast = aligned && a.K == 2048 * nb && (nb == 1 || scale_vec_ok(nb, a.K / kBlkElems, a.s1, a.s3));
-    const int W = nb == 1 ? 4 : sh.t1_waves;
-    return fast && nb <= 2 && !sh.pipe && sh.t1 && a.hidden % (W * 4) == 0 && aligned16(a.s1) &&
-           aligned16(a.s3);
+    return fast && nb <= 2 && a.hidden % (kT1Waves * 4) == 0 && aligned16(a.s1) && aligned16(a.s3);
 }
 
 // gate: the one-token kernel also routes (1: ranks a.gate.logits; 2: takes
-// a.gate.ids_in / w_in); requires stage_a_t1_ok.
+// a.gate.ids_in / w_in); requires stage_a_t1_ok and INDEXED.
 template <bool INDEXED, bool ALIGNED, bool MULTI>
 hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, int gate = 0) {
-    const Shapes& sh = shapes();
     const int nb = blocks_per_lane(a.K);
     a.scale_vec = scale_vec_ok(nb, a.K / kBlkElems, a.s1, a.s3);
     const bool fast = ALIGNED && a.K == 2048 * nb && (nb == 1 || a.scale_vec);
-    const int hc = fast ? sh.hc : 2;
-    const bool pipe = fast && sh.pipe;
-    a.h_per_wave = pipe ? sh.h_per_wave : hc;
-    dim3 grid((unsigned)((a.hidden + kWavesA * a.h_per_wave - 1) / (kWavesA * a.h_per_wave)),
-              (unsigned)slots);
-    dim3 block(64 * kWavesA);
-#define DSV4_A(NBV, HCV, FASTV, PIPEV) \
-    hipLaunchKernelGGL((moe_swiglu_kernel<NBV, HCV, INDEXED, FASTV, PIPEV, MULTI>), grid, block, 0, stream, a)
-    // The one-token kernel takes whole tiles of W*4 rows and reads each
-    // tile's scales with 16-byte loads.
-    const int W = nb == 1 ? 4 : sh.t1_waves;
     const bool t1 = !MULTI && stage_a_t1_ok(a, ALIGNED);
     if (gate && !(t1 && INDEXED)) return hipErrorInvalidValue;
     // Several tokens on the FAST path: the multi-token kernel (whole tiles of
     // 16 rows, 16-byte aligned scale rows).
-    const bool tn = MULTI && INDEXED && fast && nb <= 2 && sh.tn > 0 && a.hidden % 16 == 0 &&
-                    aligned16(a.s1) && aligned16(a.s3);
+    const bool tn = MULTI && INDEXED && fast && nb <= 2 && a.hidden % 16 == 0 && aligned16(a.s1) &&
+                    aligned16(a.s3);
     if (tn) {
-        dim3 gn((unsigned)(a.hidden / 16), (unsigned)slots);
-#define DSV4_TN(NBV)                                                                                    \
-    if (sh.tn == 2) hipLaunchKernelGGL((moe_swiglu_tn_kernel<NBV, 4, 4, 2>), gn, dim3(256), 0, stream, a); \
-    else hipLaunchKernelGGL((moe_swiglu_tn_kernel<NBV, 4, 4, 1>), gn, dim3(256), 0, stream, a);
-        if (nb == 1) { DSV4_TN(1) }
-        else { DSV4_TN(2) }
-#undef DSV4_TN
-    } else if (t1) {
-        dim3 g1((unsigned)(a.hidden / (W * 4)), (unsigned)slots);
-#define DSV4_T1(NBV, WV)                                                                                   \
-    if (gate == 1) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED ? 1 : 0>), g1,  \
-                                      dim3(64 * WV), 0, stream, a);                                         \
-    else if (gate == 2) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, INDEXED ? 2 : 0>), \
-                                           g1, dim3(64 * WV), 0, stream, a);                                \
-    else hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, WV, 4, 0>), g1, dim3(64 * WV), 0, stream, a);
-        if (nb == 1) { DSV4_T1(1, 4) }
-        else if (W == 4) { DSV4_T1(2, 4) }
-        else if (W == 8) { DSV4_T1(2, 8) }
-        else { DSV4_T1(2, 16) }
+        const dim3 gn((unsigned)(a.hidden / 16), (unsigned)slots);
+        if (nb == 1) hipLaunchKernelGGL((moe_swiglu_tn_kernel<1, 4, 4, 2>), gn, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((moe_swiglu_tn_kernel<2, 4, 4, 2>), gn, dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
+    if (t1) {
+        const dim3 g1((unsigned)(a.hidden / (kT1Waves * 4)), (unsigned)slots);
+        const dim3 b1(64 * kT1Waves);
+#define DSV4_T1(NBV)                                                                                              \
+    if (gate == 1) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, kT1Waves, 4, INDEXED ? 1 : 0>), g1, b1, \
+                                      0, stream, a);                                                             \
+    else if (gate == 2) hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, kT1Waves, 4, INDEXED ? 2 : 0>),  \
+                                           g1, b1, 0, stream, a);                                                 \
+    else hipLaunchKernelGGL((moe_swiglu_t1_kernel<NBV, 4, INDEXED, kT1Waves, 4, 0>), g1, b1, 0, stream, a);
+        if (nb == 1) { DSV4_T1(1) }
+        else { DSV4_T1(2) }
 #undef DSV4_T1
-    } else if (!fast) {
-        if (nb == 1) DSV4_A(1, 2, false, false);
-        else if (nb == 2) DSV4_A(2, 2, false, false);
-        else return hipErrorInvalidValue;
-    } else if (nb == 1) {
-        DSV4_A(1, 4, true, false);
+        return hipGetLastError();
+    }
+    const int hc = fast ? kChunkFast : kChunkChecked;
+    const dim3 grid((unsigned)((a.hidden + kWavesA * hc - 1) / (kWavesA * hc)), (unsigned)slots);
+    const dim3 block(64 * kWavesA);
+#define DSV4_A(NBV, HCV, FASTV) \
+    hipLaunchKernelGGL((moe_swiglu_kernel<NBV, HCV, INDEXED, FASTV, MULTI>), grid, block, 0, stream, a)
+    if (nb == 1) {
+        if (fast) DSV4_A(1, kChunkFast, true);
+        else DSV4_A(1, kChunkChecked, false);
     } else if (nb == 2) {
-        if (hc == 4 && pipe) DSV4_A(2, 4, true, true);
-        else if (hc == 4) DSV4_A(2, 4, true, false);
-        else if (pipe) DSV4_A(2, 2, true, true);
-        else DSV4_A(2, 2, true, false);
+        if (fast) DSV4_A(2, kChunkFast, true);
+        else DSV4_A(2, kChunkChecked, false);
     } else {
         return hipErrorInvalidValue;
     }
@@ -1799,69 +1690,43 @@ hipError_t launch_stage_a(StageAArgs a, int slots, hipStream_t stream, int gate 
 
 template <int TMAX, bool INDEXED, bool ALIGNED, bool MULTI>
 hipError_t launch_stage_b(StageBArgs a, hipStream_t stream) {
-    const Shapes& sh = shapes();
     const int nb = blocks_per_lane(a.hidden);
     a.scale_vec = scale_vec_ok(nb, a.hidden / kBlkElems, a.s2, a.s2);
     const bool fast = ALIGNED && a.hidden == 2048 * nb && (nb == 1 || a.scale_vec);
-    // The one-token path of the FAST kernels: whole row tiles (RB divides
-    // 16), 16-byte aligned scales (staged with one load per lane) and at most
-    // one expert slot per wave (8 waves).
-    a.stage_scales = !MULTI && a.out_dim % 16 == 0 && aligned16(a.s2) && a.es.n_slots <= 8;
-    // One token with the default shapes: the dedicated one-token kernel.
-    if (TMAX == 1 && fast && a.stage_scales && (nb == 1 || nb == 2) && sh.rb == 8 && sh.wb == 8 &&
-        !sh.bpipe && sh.b1_depth >= 8) {
+    const dim3 grid((unsigned)((a.out_dim + kRowsDown - 1) / kRowsDown));
+    const dim3 block(64 * kWavesDown);
+    // One token, whole 16-row tiles, 16-byte aligned scales (staged with one
+    // load per lane) and at most one expert slot per wave: the one-token kernel.
+    if (TMAX == 1 && fast && (nb == 1 || nb == 2) && a.out_dim % 16 == 0 && aligned16(a.s2) &&
+        a.es.n_slots <= kWavesDown) {
         if (nb == 1)
-            hipLaunchKernelGGL((moe_down_t1_kernel<1, 8, 8, INDEXED, 8>), dim3((unsigned)(a.out_dim / 8)),
-                               dim3(64 * 8), 0, stream, a);
+            hipLaunchKernelGGL((moe_down_t1_kernel<1, kRowsDown, kWavesDown, INDEXED>), grid, block, 0, stream, a);
         else
-            hipLaunchKernelGGL((moe_down_t1_kernel<2, 8, 8, INDEXED, 8>), dim3((unsigned)(a.out_dim / 8)),
-                               dim3(64 * 8), 0, stream, a);
+            hipLaunchKernelGGL((moe_down_t1_kernel<2, kRowsDown, kWavesDown, INDEXED>), grid, block, 0, stream, a);
         return hipGetLastError();
     }
     // Several tokens, one block per lane per row, whole 8-row tiles, at most
     // 64 slots per wave: the pipelined multi-token kernel.
-    if (MULTI && INDEXED && fast && nb == 1 && sh.tnb && a.out_dim % 8 == 0 && aligned16(a.s2) &&
-        a.es.n_slots <= 64 * 8 && a.T <= kMaxTokens) {
+    if (MULTI && INDEXED && fast && nb == 1 && a.out_dim % 8 == 0 && aligned16(a.s2) &&
+        a.es.n_slots <= 64 * kWavesDown && a.T <= kMaxTokens) {
         if (a.T <= 16)
-            hipLaunchKernelGGL((moe_down_tn_kernel<8, 8, 16>), dim3((unsigned)(a.out_dim / 8)), dim3(64 * 8), 0,
-                               stream, a);
+            hipLaunchKernelGGL((moe_down_tn_kernel<kRowsDown, kWavesDown, 16>), grid, block, 0, stream, a);
         else
-            hipLaunchKernelGGL((moe_down_tn_kernel<8, 8, kMaxTokens>), dim3((unsigned)(a.out_dim / 8)),
-                               dim3(64 * 8), 0, stream, a);
+            hipLaunchKernelGGL((moe_down_tn_kernel<kRowsDown, kWavesDown, kMaxTokens>), grid, block, 0, stream, a);
         return hipGetLastError();
     }
-#define DSV4_B(NBV, RBV, WBV, FASTV, PIPEV)                                                        \
-    hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, FASTV, PIPEV, MULTI>),       \
-                       dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
-#define DSV4_BD(NBV, RBV, WBV, BDV)                                                                \
-    hipLaunchKernelGGL((moe_down_kernel<NBV, RBV, WBV, TMAX, INDEXED, true, false, MULTI, BDV>),   \
-                       dim3((unsigned)((a.out_dim + RBV - 1) / RBV)), dim3(64 * WBV), 0, stream, a)
-    if (!fast) {
-        if (nb == 1) DSV4_B(1, 8, 4, false, false);
-        else if (nb == 2) DSV4_B(2, 8, 4, false, false);
-        else return hipErrorInvalidValue;
+#define DSV4_B(NBV, FASTV) \
+    hipLaunchKernelGGL((moe_down_kernel<NBV, kRowsDown, kWavesDown, TMAX, INDEXED, FASTV, MULTI>), grid, block, 0, stream, a)
+    if (nb == 1) {
+        if (fast) DSV4_B(1, true);
+        else DSV4_B(1, false);
     } else if (nb == 2) {
-        DSV4_B(2, 8, 8, true, false);
-    } else if (nb == 1) {
-        const int key = sh.rb * 100 + sh.wb * 10 + sh.bpipe;
-        switch (key) {
-            case 840: DSV4_B(1, 8, 4, true, false); break;
-            case 841: DSV4_B(1, 8, 4, true, true); break;
-            case 881: DSV4_B(1, 8, 8, true, true); break;
-            case 1640: DSV4_B(1, 16, 4, true, false); break;
-            case 1680: DSV4_B(1, 16, 8, true, false); break;
-            default:
-                if (MULTI || sh.b1_depth >= 8) DSV4_B(1, 8, 8, true, false);
-                else if (sh.b1_depth >= 6) DSV4_BD(1, 8, 8, 6);
-                else if (sh.b1_depth >= 4) DSV4_BD(1, 8, 8, 4);
-                else DSV4_BD(1, 8, 8, 2);
-                break;
-        }
+        if (fast) DSV4_B(2, true);
+        else DSV4_B(2, false);
     } else {
         return hipErrorInvalidValue;
     }
 #undef DSV4_B
-#undef DSV4_BD
     return hipGetLastError();
 }
 
@@ -1930,9 +1795,9 @@ MoeCall moe_call(int T, int topk, int n_experts, int hidden, void* workspace) {
 
 int launch_route(const float* logits, const int32_t* ids, const float* weights, int T, int topk,
                  int n_experts, int32_t* ids_out, float* w_out, const MoeCall& c,
-                 hipStream_t stream) {
+                 hipStream_t stream, Scoring sc = Scoring{kScoreSigmoid, 1.0f}) {
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, stream, logits, ids,
-                       weights, T, topk, n_experts, ids_out, w_out, c.rt);
+                       weights, T, topk, n_experts, ids_out, w_out, c.rt, sc);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         std::fprintf(stderr, "mxfp4 moe: routing launch failed: %s\n", hipGetErrorString(e));
@@ -2000,6 +1865,72 @@ int launch_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int hi
         return -7;
     }
     return 0;
+}
+
+
+int router_validate(int T, int n_experts, int K) {
+    if (T < 1 || T > kMaxTokens || n_experts < 1 || n_experts > kMaxExperts || K < 8 || K % 8 != 0 ||
+        K > kMaxRouterK) {
+        std::fprintf(stderr, "mxfp4 router: bad T=%d n_experts=%d K=%d\n", T, n_experts, K);
+        return -1;
+    }
+    return 0;
+}
+
+int launch_router(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate, int T, int n_experts, int K,
+                  float* logits, hipStream_t stream) {
+    if (!x || !W_gate || !logits || !aligned16(x) || !aligned16(W_gate)) {
+        std::fprintf(stderr, "mxfp4 router: x, W_gate and logits must be non-null, x and W_gate 16-byte aligned\n");
+        return -3;
+    }
+    const dim3 grid((unsigned)((n_experts + kRouterWaves - 1) / kRouterWaves)), block(64 * kRouterWaves);
+    const auto* xp = reinterpret_cast<const uint16_t*>(x);
+    const auto* wp = reinterpret_cast<const uint16_t*>(W_gate);
+    const int nj = (K / 8 + 63) / 64;
+    if (nj <= 4) hipLaunchKernelGGL((moe_router_gemv_kernel<4>), grid, block, 0, stream, xp, wp, T, n_experts, K, logits);
+    else if (nj <= 8) hipLaunchKernelGGL((moe_router_gemv_kernel<8>), grid, block, 0, stream, xp, wp, T, n_experts, K, logits);
+    else hipLaunchKernelGGL((moe_router_gemv_kernel<16>), grid, block, 0, stream, xp, wp, T, n_experts, K, logits);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "mxfp4 router: launch failed: %s\n", hipGetErrorString(e));
+        return -5;
+    }
+    return 0;
+}
+
+// The routed layer from logits: gating (scored as `sc`) + stages A and B.
+// One token on the aligned path gates inside stage A (two launches).
+int moe_layer_impl(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_packed,
+                   const uint8_t* W3_packed, const uint8_t* W2_packed, const uint8_t* W1_scale,
+                   const uint8_t* W3_scale, const uint8_t* W2_scale, int T, int topk, int n_experts,
+                   int K_in, int hidden, int out_dim, dsv4_bf16_t* out, int32_t* ids_out,
+                   float* weights_out, const MoeCall& c, Scoring sc, hipStream_t stream) {
+    int v;
+    if (T == 1) {
+        StageAArgs probe{};
+        probe.K = K_in;
+        probe.hidden = hidden;
+        probe.s1 = W1_scale;
+        probe.s3 = W3_scale;
+        const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
+        if (stage_a_t1_ok(probe, al)) {
+            GateArgs g{logits, nullptr, nullptr, n_experts, topk, ids_out, weights_out, c.rt, sc};
+            v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
+            if (v != 0) return v;
+            return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+        }
+    }
+    v = launch_route(logits, nullptr, nullptr, T, topk, n_experts, ids_out, weights_out, c, stream, sc);
+    if (v != 0) return v;
+    v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
+    if (v != 0) return v;
+    return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+}
+
+// Bytes of the routed-dispatch workspace: the layer's workspace, then the
+// router logits [T, n_experts] fp32 at a 256-byte boundary.
+size_t dispatch_logits_offset(int T, int topk, int n_experts, int hidden) {
+    return align_up(moe_layout(T, topk, n_experts, hidden).total, 256);
 }
 
 }  // namespace
@@ -2097,21 +2028,43 @@ extern "C" int mxfp4_grouped_gemv_topk(const dsv4_bf16_t* x, const uint8_t* W1_p
     return 0;
 }
 
-extern "C" int mxfp4_moe_route_sigmoid_topk(const float* logits, int T, int n_experts, int topk,
-                                            int32_t* ids, float* weights, hipStream_t stream) {
+namespace {
+
+int route_topk(const float* logits, int T, int n_experts, int topk, Scoring sc, int32_t* ids,
+               float* weights, hipStream_t stream) {
     if (T < 1 || n_experts < 1 || n_experts > kMaxExperts || topk < 1 || topk > kMaxTopk ||
-        topk > n_experts) {
-        std::fprintf(stderr, "mxfp4 route: bad T=%d n_experts=%d topk=%d\n", T, n_experts, topk);
+        topk > n_experts || (sc.mode != kScoreSigmoid && sc.mode != kScoreSqrtSoftplus)) {
+        std::fprintf(stderr, "mxfp4 route: bad T=%d n_experts=%d topk=%d score_mode=%d\n", T, n_experts,
+                     topk, sc.mode);
         return -1;
     }
-    hipLaunchKernelGGL(moe_route_sigmoid_topk_kernel, dim3((unsigned)T), dim3(64), 0, stream,
-                       logits, n_experts, topk, ids, weights);
+    hipLaunchKernelGGL(moe_route_topk_kernel, dim3((unsigned)T), dim3(64), 0, stream, logits, n_experts,
+                       topk, sc, ids, weights);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         std::fprintf(stderr, "mxfp4 route: launch failed: %s\n", hipGetErrorString(e));
         return -5;
     }
     return 0;
+}
+
+}  // namespace
+
+extern "C" int mxfp4_moe_route_sigmoid_topk(const float* logits, int T, int n_experts, int topk,
+                                            int32_t* ids, float* weights, hipStream_t stream) {
+    return route_topk(logits, T, n_experts, topk, Scoring{kScoreSigmoid, 1.0f}, ids, weights, stream);
+}
+
+extern "C" int mxfp4_moe_route_topk(const float* logits, int T, int n_experts, int topk, int score_mode,
+                                    float routed_scale, int32_t* ids, float* weights, hipStream_t stream) {
+    return route_topk(logits, T, n_experts, topk, Scoring{score_mode, routed_scale}, ids, weights, stream);
+}
+
+extern "C" int mxfp4_moe_router_logits(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate, int T, int n_experts,
+                                       int K, float* logits, hipStream_t stream) {
+    const int v = router_validate(T, n_experts, K);
+    if (v != 0) return v;
+    return launch_router(x, W_gate, T, n_experts, K, logits, stream);
 }
 
 extern "C" size_t mxfp4_moe_workspace_bytes(int T, int topk, int n_experts, int hidden) {
@@ -2168,7 +2121,7 @@ extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_pa
         probe.s3 = W3_scale;
         const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
         if (stage_a_t1_ok(probe, al)) {
-            GateArgs g{nullptr, ids, weights, n_experts, topk, nullptr, nullptr, c.rt};
+            GateArgs g{nullptr, ids, weights, n_experts, topk, nullptr, nullptr, c.rt, Scoring{kScoreSigmoid, 1.0f}};
             v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
             if (v != 0) return v;
             return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
@@ -2188,28 +2141,41 @@ extern "C" int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
                                int n_experts, int K_in, int hidden, int out_dim, dsv4_bf16_t* out,
                                int32_t* ids_out, float* weights_out, void* workspace,
                                hipStream_t stream) {
-    int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
+    const int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
     if (v != 0) return v;
     if (topk > n_experts) return -4;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
-    if (T == 1 && (ids_out == nullptr) == (weights_out == nullptr)) {
-        // One token: the gating runs inside stage A (two launches in all).
-        StageAArgs probe{};
-        probe.K = K_in;
-        probe.hidden = hidden;
-        probe.s1 = W1_scale;
-        probe.s3 = W3_scale;
-        const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
-        if (stage_a_t1_ok(probe, al)) {
-            GateArgs g{logits, nullptr, nullptr, n_experts, topk, ids_out, weights_out, c.rt};
-            v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
-            if (v != 0) return v;
-            return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
-        }
+    return moe_layer_impl(x, logits, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale, T, topk,
+                          n_experts, K_in, hidden, out_dim, out, ids_out, weights_out, c,
+                          Scoring{kScoreSigmoid, 1.0f}, stream);
+}
+
+extern "C" size_t mxfp4_moe_dispatch_workspace_bytes(int T, int topk, int n_experts, int hidden) {
+    if (T < 1 || topk < 1 || n_experts < 1 || hidden < 1) return 0;
+    return dispatch_logits_offset(T, topk, n_experts, hidden) + (size_t)T * n_experts * sizeof(float) + 256;
+}
+
+extern "C" int mxfp4_moe_routed_dispatch(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate,
+                                         const uint8_t* W1_packed, const uint8_t* W3_packed,
+                                         const uint8_t* W2_packed, const uint8_t* W1_scale,
+                                         const uint8_t* W3_scale, const uint8_t* W2_scale, int T, int topk,
+                                         int n_experts, int K_in, int hidden, int out_dim, float routed_scale,
+                                         dsv4_bf16_t* out, int32_t* ids_out, float* weights_out,
+                                         void* workspace, hipStream_t stream) {
+    int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
+    if (v != 0) return v;
+    if (topk > n_experts) return -4;
+    if (router_validate(T, n_experts, K_in) != 0) return -4;
+    if (!workspace || !out) {
+        std::fprintf(stderr, "mxfp4 dispatch: null workspace or out\n");
+        return -3;
     }
-    v = launch_route(logits, nullptr, nullptr, T, topk, n_experts, ids_out, weights_out, c, stream);
-    if (v != 0) return v;
-    v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
-    if (v != 0) return v;
-    return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+    const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
+    uint8_t* base = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(workspace), 256));
+    float* logits = reinterpret_cast<float*>(base + dispatch_logits_offset(T, topk, n_experts, hidden));
+    v = launch_router(x, W_gate, T, n_experts, K_in, logits, stream);
+    if (v != 0) return v == -3 ? -3 : -5;
+    return moe_layer_impl(x, logits, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale, T, topk,
+                          n_experts, K_in, hidden, out_dim, out, ids_out, weights_out, c,
+                          Scoring{kScoreSqrtSoftplus, routed_scale}, stream);
 }

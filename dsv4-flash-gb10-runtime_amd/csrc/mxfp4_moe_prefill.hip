@@ -159,15 +159,20 @@ struct GemmArgs {
 
 // 16 bytes of e2m1 codes (one MX block) -> 32 bf16 in 4 operands of 8
 // (elements 8j..8j+7 in op[j]), times the block scale 2^(s-127) applied by
-// the conversion itself (exact for bytes 1..254). Scale byte 0xFF decodes to
-// a scale of 0, and so does byte 0 (2^-127 is an fp32 subnormal): every
-// element is then a zero, whose sign cannot change an fp32 sum that starts
-// at +0.
+// the conversion itself: exact for every byte, since every code times a
+// power of two in [2^-127, 2^127] is a bf16 value. The conversion takes the
+// scale from the exponent field of its fp32 operand (an E8M0 value), so the
+// byte goes straight into that field: byte 0 gives 2^-127, as the decode path
+// and reference runtime/e8m0_decode.py:8 do. Byte 0xFF decodes to a scale of 0
+// (the kernels' convention): its codes keep only their sign bits (code 8 is
+// -0), which the conversion turns into signed zeros.
 __device__ __forceinline__ void dequant_block(u32x4 w, uint32_t s, bf16x8* op) {
-    const float scale = __uint_as_float(s == 0xFFu ? 0u : (s << 23));
+    const bool zero = s == 0xFFu;
+    const float scale = __uint_as_float(zero ? 0u : (s << 23));
+    const uint32_t keep = zero ? 0x88888888u : 0xFFFFFFFFu;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t d = w[q];
+        const uint32_t d = w[q] & keep;
         const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0);
         const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1);
         const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2);
@@ -468,6 +473,33 @@ int prefill_validate(int T, int topk, int n_experts, int K_in, int hidden, int o
 }
 
 }  // namespace
+
+namespace {
+
+// One thread per MX block: the prefill GEMMs' own decode (dequant_block).
+__global__ __launch_bounds__(256) void prefill_dequant_kernel(const uint8_t* w, const uint8_t* s, int nblk,
+                                                              int64_t total, uint16_t* out) {
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= total) return;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(w + 16 * b);
+    bf16x8 op[4];
+    dequant_block(v, s[b], op);
+    u32x4* o = reinterpret_cast<u32x4*>(out + 32 * b);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = __builtin_bit_cast(u32x4, op[q]);
+}
+
+}  // namespace
+
+extern "C" int mxfp4_moe_prefill_dequant_bf16(const uint8_t* W_packed, const uint8_t* W_scale, int K, int N,
+                                              dsv4_bf16_t* out, hipStream_t stream) {
+    if (K % kBlk != 0 || K < kBlk) return -1;
+    if (N < 1 || !W_packed || !W_scale || !out || !aligned16(W_packed) || !aligned16(out)) return -3;
+    const int64_t total = (int64_t)N * (K / kBlk);
+    hipLaunchKernelGGL(prefill_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       W_packed, W_scale, K / kBlk, total, reinterpret_cast<uint16_t*>(out));
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
 
 extern "C" size_t mxfp4_moe_prefill_workspace_bytes(int T, int topk, int n_experts, int hidden,
                                                     int out_dim) {

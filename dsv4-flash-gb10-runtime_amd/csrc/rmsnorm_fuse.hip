@@ -9,7 +9,8 @@
 // One workgroup (256 threads = 4 waves) per row. Each thread keeps its slice
 // of the row in registers (8 bf16 per 16-byte load, at most 32 values per
 // thread for H <= 8192), so the row is read once; the sum of squares is
-// reduced with wave shuffles and a 4-entry LDS exchange.
+// reduced with wave shuffles and a 4-entry LDS exchange. The norm weight is
+// loaded together with the row, before the reduction.
 
 #include <cstdint>
 
@@ -52,8 +53,12 @@ __device__ __forceinline__ u32x4 pack8(const uint16_t* h) {
     return r;
 }
 
-// Vector path: rows 16-byte aligned and H % 8 == 0.
-template <bool RESID>
+// Vector path: rows 16-byte aligned and H % 8 == 0; NV = ceil(H / 2048)
+// 16-byte pieces per thread. Every load (row, residual and weight pieces) is
+// issued up front, unconditionally (indices clamped into the row), so the
+// weight is in flight with the row and the whole kernel waits on one memory
+// round trip before the reduction.
+template <bool RESID, int NV>
 __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const uint16_t* x, const uint16_t* res,
                                                                const uint16_t* w, uint16_t* y,
                                                                uint16_t* new_res, int hidden,
@@ -61,17 +66,25 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const uint16_t* x
     __shared__ float red[kThreads / 64];
     const int64_t off = (int64_t)blockIdx.x * hidden;
     const int nvec = hidden / kVec;
-    float v[kMaxVecPerThread][kVec];
+    u32x4 xv[NV], rv[NV], gv[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int64_t i = min((int)threadIdx.x + c * kThreads, nvec - 1);
+        xv[c] = *reinterpret_cast<const u32x4*>(x + off + i * kVec);
+        if constexpr (RESID) rv[c] = *reinterpret_cast<const u32x4*>(res + off + i * kVec);
+        gv[c] = *reinterpret_cast<const u32x4*>(w + i * kVec);
+    }
+    float v[NV][kVec];
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < kMaxVecPerThread; ++c) {
+    for (int c = 0; c < NV; ++c) {
         const int i = threadIdx.x + c * kThreads;
         if (i < nvec) {
             float a[kVec];
-            unpack8(*reinterpret_cast<const u32x4*>(x + off + (int64_t)i * kVec), a);
+            unpack8(xv[c], a);
             if constexpr (RESID) {
                 float b[kVec];
-                unpack8(*reinterpret_cast<const u32x4*>(res + off + (int64_t)i * kVec), b);
+                unpack8(rv[c], b);
                 uint16_t tb[kVec];
 #pragma unroll
                 for (int e = 0; e < kVec; ++e) {
@@ -93,17 +106,28 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const uint16_t* x
     const float total = block_sum(ss, red);
     const float rms = rsqrtf(total * (1.0f / (float)hidden) + eps);
 #pragma unroll
-    for (int c = 0; c < kMaxVecPerThread; ++c) {
+    for (int c = 0; c < NV; ++c) {
         const int i = threadIdx.x + c * kThreads;
         if (i < nvec) {
             float g[kVec];
-            unpack8(*reinterpret_cast<const u32x4*>(w + (int64_t)i * kVec), g);
+            unpack8(gv[c], g);
             uint16_t o[kVec];
 #pragma unroll
             for (int e = 0; e < kVec; ++e) o[e] = f32_to_bf16_bits((g[e] * v[c][e]) * rms);
             *reinterpret_cast<u32x4*>(y + off + (int64_t)i * kVec) = pack8(o);
         }
     }
+}
+
+template <bool RESID>
+void launch_vec(const uint16_t* x, const uint16_t* res, const uint16_t* w, uint16_t* y, uint16_t* new_res,
+                int n_rows, int hidden, float eps, hipStream_t stream) {
+    const int nv = (hidden / kVec + kThreads - 1) / kThreads;
+    const dim3 grid((unsigned)n_rows), block(kThreads);
+    if (nv <= 1) hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 1>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
+    else if (nv == 2) hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 2>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
+    else if (nv == 3) hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 3>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
+    else hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 4>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
 }
 
 // Scalar path for any alignment / H: each thread walks h = tid, tid+256, ...
@@ -158,8 +182,7 @@ extern "C" int rmsnorm_fuse_fwd(const void* x, const void* weight, void* y, int 
     auto* yp = static_cast<uint16_t*>(y);
     const bool vec = hidden % kVec == 0 && aligned16(x) && aligned16(weight) && aligned16(y);
     if (vec)
-        hipLaunchKernelGGL(rmsnorm_vec_kernel<false>, dim3((unsigned)n_rows), dim3(kThreads), 0,
-                           stream, xp, nullptr, wp, yp, nullptr, hidden, eps);
+        launch_vec<false>(xp, nullptr, wp, yp, nullptr, n_rows, hidden, eps, stream);
     else
         hipLaunchKernelGGL(rmsnorm_scalar_kernel<false>, dim3((unsigned)n_rows), dim3(kThreads), 0,
                            stream, xp, nullptr, wp, yp, nullptr, hidden, eps);
@@ -179,8 +202,7 @@ extern "C" int rmsnorm_fuse_residual_add(const void* x, const void* residual, co
     const bool vec = hidden % kVec == 0 && aligned16(x) && aligned16(residual) &&
                      aligned16(weight) && aligned16(y_norm) && aligned16(new_residual);
     if (vec)
-        hipLaunchKernelGGL(rmsnorm_vec_kernel<true>, dim3((unsigned)n_rows), dim3(kThreads), 0,
-                           stream, xp, rp, wp, yp, np, hidden, eps);
+        launch_vec<true>(xp, rp, wp, yp, np, n_rows, hidden, eps, stream);
     else
         hipLaunchKernelGGL(rmsnorm_scalar_kernel<true>, dim3((unsigned)n_rows), dim3(kThreads), 0,
                            stream, xp, rp, wp, yp, np, hidden, eps);

@@ -83,17 +83,29 @@ def expert_host_weights(seed_base: int, e: int, K: int, hidden: int, out_dim: in
 
 
 class RoutedMoELayer:
-    """Device-resident routed MoE layer: forward(x, logits) -> bf16 [T, out_dim]."""
+    """Device-resident routed MoE layer -> bf16 [T, out_dim]:
+        forward(x, logits=...)          config gating (sigmoid top-k renormalised);
+        forward(x, ids=..., weights=...) the caller's routing;
+        forward(x)                      with router_gate [E, K] bf16 given: the
+                                        reference engine's routing (router GEMV,
+                                        sqrt-softplus top-k x routed_scale),
+                                        kernel/cpp-engine-mxfp4/routed.cu:373-503."""
 
     def __init__(self, weights: MoEWeights, topk: int = 8, max_tokens: int = 16,
-                 check: bool = True):
+                 check: bool = True, router_gate: Optional[torch.Tensor] = None,
+                 routed_scale: float = 1.5):
         self.w = weights
         self.check = check
         self.topk = topk
         self.max_tokens = max_tokens
+        self.router_gate = router_gate
+        self.routed_scale = routed_scale
         dev = weights.W1["packed"].device
         self.device = dev
-        ws = gb.moe_workspace_bytes(max_tokens, topk, weights.n_experts, weights.hidden)
+        if router_gate is not None:
+            ws = gb.dispatch_workspace_bytes(max_tokens, topk, weights.n_experts, weights.hidden)
+        else:
+            ws = gb.moe_workspace_bytes(max_tokens, topk, weights.n_experts, weights.hidden)
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
         self.ids = torch.empty(max_tokens, topk, dtype=torch.int32, device=dev)
         self.weights = torch.empty(max_tokens, topk, dtype=torch.float32, device=dev)
@@ -116,7 +128,12 @@ class RoutedMoELayer:
                                       out=self.out[:T], ids_out=self.ids[:T],
                                       weights_out=self.weights[:T], workspace=self.workspace,
                                       check=self.check)
+        if ids is None and weights is None and self.router_gate is not None:
+            return gb.mxfp4_moe_routed_dispatch(x, self.router_gate, self.w.W1, self.w.W3, self.w.W2,
+                                                self.topk, self.routed_scale, out=self.out[:T],
+                                                ids_out=self.ids[:T], weights_out=self.weights[:T],
+                                                workspace=self.workspace)
         if ids is None or weights is None:
-            raise ValueError("pass logits, or ids and weights")
+            raise ValueError("pass logits, or ids and weights (or build the layer with a router_gate)")
         return gb.mxfp4_moe_grouped_gemv(x, self.w.W1, self.w.W3, self.w.W2, ids, weights,
                                          out=self.out[:T], workspace=self.workspace)

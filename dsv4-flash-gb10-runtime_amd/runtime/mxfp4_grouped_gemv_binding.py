@@ -13,6 +13,11 @@ runtime/mxfp4_grouped_gemv_binding.py:95-174):
 Extensions (not in the reference):
 
     route_sigmoid_topk(logits [T, E] f32, topk) -> (ids [T, topk] int32, weights [T, topk] f32)
+    route_topk(logits, topk, score_mode, routed_scale) -> (ids, weights)   (either gating)
+    router_logits(x [T, K] bf16, W_gate [E, K] bf16) -> logits [T, E] f32
+    mxfp4_moe_routed_dispatch(x, W_gate, W1, W3, W2, topk, routed_scale=1.5)
+        the reference engine's routed dispatch (router GEMV + sqrt-softplus
+        top-k + grouped GEMV) on the device
     mxfp4_moe_grouped_gemv(x [T, K_in], W1, W3, W2, ids, weights, out=None, workspace=None)
         experts read in place from per-layer tensors [n_experts, ...].
 
@@ -67,6 +72,17 @@ def _load_lib() -> ctypes.CDLL:
     lib.mxfp4_moe_prefill_workspace_bytes.argtypes = [_c_int] * 5
     lib.mxfp4_moe_prefill.restype = _c_int
     lib.mxfp4_moe_prefill.argtypes = [_c_void_p] * 9 + [_c_int] * 6 + [_c_void_p] * 3
+    lib.mxfp4_moe_prefill_dequant_bf16.restype = _c_int
+    lib.mxfp4_moe_prefill_dequant_bf16.argtypes = [_c_void_p] * 2 + [_c_int] * 2 + [_c_void_p] * 2
+    lib.mxfp4_moe_route_topk.restype = _c_int
+    lib.mxfp4_moe_route_topk.argtypes = [_c_void_p] + [_c_int] * 4 + [ctypes.c_float] + [_c_void_p] * 3
+    lib.mxfp4_moe_router_logits.restype = _c_int
+    lib.mxfp4_moe_router_logits.argtypes = [_c_void_p] * 2 + [_c_int] * 3 + [_c_void_p] * 2
+    lib.mxfp4_moe_dispatch_workspace_bytes.restype = _c_size_t
+    lib.mxfp4_moe_dispatch_workspace_bytes.argtypes = [_c_int] * 4
+    lib.mxfp4_moe_routed_dispatch.restype = _c_int
+    lib.mxfp4_moe_routed_dispatch.argtypes = ([_c_void_p] * 8 + [_c_int] * 6 + [ctypes.c_float] +
+                                             [_c_void_p] * 5)
     _LIB = lib
     return lib
 
@@ -180,6 +196,129 @@ def route_sigmoid_topk(logits: torch.Tensor, topk: int,
     if rc != 0:
         raise RuntimeError(f"mxfp4_moe_route_sigmoid_topk returned {rc}")
     return ids, weights
+
+
+SCORE_SIGMOID = 0          # benchmark configuration gating
+SCORE_SQRT_SOFTPLUS = 1    # the reference engine's router (routed.cu:156-208)
+
+
+def route_topk(logits: torch.Tensor, topk: int, score_mode: int = SCORE_SQRT_SOFTPLUS,
+               routed_scale: float = 1.5, ids: Optional[torch.Tensor] = None,
+               weights: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Device gating of logits [T, E] with a choice of scoring (SCORE_SIGMOID or
+    SCORE_SQRT_SOFTPLUS with routed_scale); returns (ids, weights) [T, topk]."""
+    lib = _load_lib()
+    _check(logits, "logits", torch.float32)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [T, n_experts]")
+    T, E = logits.shape
+    if ids is None:
+        ids = torch.empty(T, topk, dtype=torch.int32, device=logits.device)
+    if weights is None:
+        weights = torch.empty(T, topk, dtype=torch.float32, device=logits.device)
+    _check(ids, "ids", torch.int32)
+    _check(weights, "weights", torch.float32)
+    rc = lib.mxfp4_moe_route_topk(_lib.vp(logits), T, E, topk, int(score_mode), float(routed_scale),
+                                  _lib.vp(ids), _lib.vp(weights),
+                                  ctypes.c_void_p(_lib.stream_ptr(logits.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_route_topk returned {rc}")
+    return ids, weights
+
+
+def router_logits(x: torch.Tensor, W_gate: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Router gate GEMV: logits [T, E] fp32 = x [T, K] bf16 @ W_gate [E, K] bf16 ^T."""
+    lib = _load_lib()
+    _check(x, "x", torch.bfloat16)
+    _check(W_gate, "W_gate", torch.bfloat16)
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    T, K = x.shape
+    if W_gate.dim() != 2 or W_gate.shape[1] != K:
+        raise ValueError(f"W_gate shape {tuple(W_gate.shape)} != (n_experts, {K})")
+    E = W_gate.shape[0]
+    if out is None:
+        out = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    _check(out, "out", torch.float32)
+    if out.numel() != T * E:
+        raise ValueError(f"out numel {out.numel()} != {T * E}")
+    rc = lib.mxfp4_moe_router_logits(_lib.vp(x), _lib.vp(W_gate), T, E, K, _lib.vp(out),
+                                     ctypes.c_void_p(_lib.stream_ptr(x.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_router_logits returned {rc}")
+    return out
+
+
+def dispatch_workspace_bytes(T: int, topk: int, n_experts: int, hidden: int) -> int:
+    return int(_load_lib().mxfp4_moe_dispatch_workspace_bytes(T, topk, n_experts, hidden))
+
+
+def mxfp4_moe_routed_dispatch(
+    x: torch.Tensor,
+    W_gate: torch.Tensor,
+    W1: Dict[str, torch.Tensor],
+    W3: Dict[str, torch.Tensor],
+    W2: Dict[str, torch.Tensor],
+    topk: int,
+    routed_scale: float = 1.5,
+    out: Optional[torch.Tensor] = None,
+    ids_out: Optional[torch.Tensor] = None,
+    weights_out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """The reference engine's routed dispatch on the device (router GEMV,
+    sqrt-softplus top-k x routed_scale, expert-indexed grouped GEMV) for
+    x [T, K_in]; returns bf16 [T, out_dim]."""
+    lib = _load_lib()
+    _check(x, "x", torch.bfloat16)
+    _check(W_gate, "W_gate", torch.bfloat16)
+    _check_mats(W1, W3, W2)
+    if x.dim() == 1:
+        x = x.view(1, -1)
+    T, K_in = x.shape
+    n_experts, hidden, out_dim = _shapes(W1, W3, W2, K_in)
+    if tuple(W_gate.shape) != (n_experts, K_in):
+        raise ValueError(f"W_gate shape {tuple(W_gate.shape)} != ({n_experts}, {K_in})")
+    if out is None:
+        out = torch.empty(T, out_dim, dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    if out.numel() != T * out_dim:
+        raise ValueError(f"out numel {out.numel()} != {T * out_dim}")
+    need = lib.mxfp4_moe_dispatch_workspace_bytes(T, topk, n_experts, hidden)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace smaller than {need} bytes")
+    for name, t, dt in (("ids_out", ids_out, torch.int32), ("weights_out", weights_out, torch.float32)):
+        if t is not None:
+            _check(t, name, dt)
+            if t.numel() != T * topk:
+                raise ValueError(f"{name} numel {t.numel()} != {T * topk}")
+    rc = lib.mxfp4_moe_routed_dispatch(
+        _lib.vp(x), _lib.vp(W_gate), _lib.vp(W1["packed"]), _lib.vp(W3["packed"]), _lib.vp(W2["packed"]),
+        _lib.vp(W1["scale"]), _lib.vp(W3["scale"]), _lib.vp(W2["scale"]), T, topk, n_experts, K_in, hidden,
+        out_dim, float(routed_scale), _lib.vp(out), None if ids_out is None else _lib.vp(ids_out),
+        None if weights_out is None else _lib.vp(weights_out), _lib.vp(workspace),
+        ctypes.c_void_p(_lib.stream_ptr(x.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_routed_dispatch returned {rc}")
+    return out
+
+
+def prefill_dequant(W_packed: torch.Tensor, W_scale: torch.Tensor) -> torch.Tensor:
+    """Debug: [N, K/2] + [N, K/32] -> bf16 [N, K] with the prefill GEMMs' decode."""
+    lib = _load_lib()
+    _check(W_packed, "W_packed", torch.uint8)
+    _check(W_scale, "W_scale", torch.uint8)
+    N, K = W_packed.shape[0], W_packed.shape[1] * 2
+    if tuple(W_scale.shape) != (N, K // MXFP4_BLOCK_ELEMS):
+        raise ValueError(f"W_scale shape {tuple(W_scale.shape)} != ({N}, {K // MXFP4_BLOCK_ELEMS})")
+    out = torch.empty(N, K, dtype=torch.bfloat16, device=W_packed.device)
+    rc = lib.mxfp4_moe_prefill_dequant_bf16(_lib.vp(W_packed), _lib.vp(W_scale), K, N, _lib.vp(out),
+                                            ctypes.c_void_p(_lib.stream_ptr(W_packed.device)))
+    if rc != 0:
+        raise RuntimeError(f"mxfp4_moe_prefill_dequant_bf16 returned {rc}")
+    return out
 
 
 def moe_workspace_bytes(T: int, topk: int, n_experts: int, hidden: int) -> int:
@@ -384,4 +523,6 @@ class MoEStages:
 
 
 __all__ = ["mxfp4_grouped_gemv", "MoEStages", "mxfp4_moe_layer", "MXFP4_BLOCK_ELEMS", "route_sigmoid_topk",
-           "mxfp4_moe_grouped_gemv", "moe_workspace_bytes", "workspace_bytes"]
+           "mxfp4_moe_grouped_gemv", "moe_workspace_bytes", "workspace_bytes", "route_topk", "router_logits",
+           "mxfp4_moe_routed_dispatch", "dispatch_workspace_bytes", "prefill_dequant", "SCORE_SIGMOID",
+           "SCORE_SQRT_SOFTPLUS"]

@@ -79,6 +79,37 @@ size_t mxfp4_grouped_workspace_bytes(int n_exp, int hidden, int out_dim);
 int mxfp4_moe_route_sigmoid_topk(const float* logits, int T, int n_experts, int topk,
                                  int32_t* ids, float* weights, hipStream_t stream);
 
+/* EXTENSION: device gating with a choice of scoring, for T tokens:
+ *   score_mode 0: rank the logits; weights[t,k] = sigmoid(l_k) / sum_k' sigmoid(l_k')
+ *                 (as mxfp4_moe_route_sigmoid_topk; routed_scale is ignored);
+ *   score_mode 1: the reference router (kernel/cpp-engine-mxfp4/routed.cu:156-208,
+ *                 runtime/dsv4_engine_mxfp4.py:363-370): scores
+ *                 s = sqrt(softplus(l)), softplus(l) = max(l,0) + log1p(exp(-|l|));
+ *                 rank the scores; weights[t,k] = (s_k / (sum_k' s_k' + 1e-20f))
+ *                 * routed_scale, evaluated in double (sum in pick order) and
+ *                 rounded to float as the reference's host code does (it keeps
+ *                 fp32 weights, routed.cu:205; the Python engine rounds them to
+ *                 bf16, dsv4_engine_mxfp4.py:369).
+ * Ranking is descending, ties to the lower expert index; NaN ranks below every
+ * number (the reference never picks NaN and aborts when fewer than topk
+ * numbers exist; here NaN entries then fill the last picks). Replaces the
+ * sqrt_softplus_kernel launch, the D2H copy, the stream sync and
+ * topk6_norm_scale_host of routed.cu:156-208, 418-446. Returns 0; -1 bad
+ * T/n_experts/topk/score_mode (as mxfp4_moe_route_sigmoid_topk); -5 launch
+ * failure. */
+int mxfp4_moe_route_topk(const float* logits, int T, int n_experts, int topk, int score_mode,
+                         float routed_scale, int32_t* ids, float* weights, hipStream_t stream);
+
+/* EXTENSION: the router gate GEMV, logits[t, n] = sum_k W_gate[n, k] * x[t, k]
+ * (bf16 operands, fp32 accumulate and output), x [T, K], W_gate [n_experts, K]
+ * row-major, logits [T, n_experts]. Replaces router_gate_gemv_kernel,
+ * reference kernel/cpp-engine-mxfp4/routed.cu:124-153 (launched at :401-410
+ * and by dsv4_routed_compute_router_logits_isolated, :614-636). Returns 0; -1
+ * T outside [1, 64], n_experts outside [1, 1024], K not a positive multiple of
+ * 8 or K > 8192; -3 x or W_gate not 16-byte aligned; -5 launch failure. */
+int mxfp4_moe_router_logits(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate, int T, int n_experts,
+                            int K, float* logits, hipStream_t stream);
+
 /* EXTENSION: workspace bytes for mxfp4_moe_grouped_gemv. */
 size_t mxfp4_moe_workspace_bytes(int T, int topk, int n_experts, int hidden);
 
@@ -126,8 +157,8 @@ int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int
 /* EXTENSION: one routed-MoE layer at decode in one call (three launches on
  * `stream`): device gating of logits [T, n_experts] (top-`topk`, sigmoid
  * weights renormalised to 1, as mxfp4_moe_route_sigmoid_topk), then stages A
- * and B of mxfp4_moe_grouped_gemv. ids_out / weights_out ([T, topk], may be
- * NULL) receive the routing. Workspace as mxfp4_moe_grouped_gemv. Return codes
+ * and B of mxfp4_moe_grouped_gemv. ids_out / weights_out ([T, topk]; either
+ * or both may be NULL) receive the routing. Workspace as mxfp4_moe_grouped_gemv. Return codes
  * as mxfp4_moe_grouped_gemv (-4 also for topk > n_experts). */
 int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
                     const uint8_t* W1_packed, const uint8_t* W3_packed, const uint8_t* W2_packed,
@@ -135,6 +166,25 @@ int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
                     int T, int topk, int n_experts, int K_in, int hidden, int out_dim,
                     dsv4_bf16_t* out, int32_t* ids_out, float* weights_out, void* workspace,
                     hipStream_t stream);
+
+/* EXTENSION: the reference's routed dispatch of one MoE layer on the device
+ * (replaces dsv4_routed_dispatch, reference kernel/cpp-engine-mxfp4/routed.cu:373-503,
+ * for T tokens): the router gate GEMV (mxfp4_moe_router_logits over x), the
+ * reference's scoring (mxfp4_moe_route_topk score_mode 1 with routed_scale,
+ * 1.5 in the reference) and stages A and B of mxfp4_moe_grouped_gemv, with the
+ * experts read in place from the per-layer tensors. No host sync, no pack
+ * copies; three launches for one token (the scoring runs inside stage A), four
+ * otherwise. W_gate [n_experts, K_in] bf16; ids_out / weights_out as
+ * mxfp4_moe_layer. Workspace of mxfp4_moe_dispatch_workspace_bytes bytes.
+ * Returns as mxfp4_moe_layer, plus -3 for an unaligned x or W_gate and -4 for
+ * T, n_experts or K_in outside the router's limits. */
+size_t mxfp4_moe_dispatch_workspace_bytes(int T, int topk, int n_experts, int hidden);
+int mxfp4_moe_routed_dispatch(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate,
+                              const uint8_t* W1_packed, const uint8_t* W3_packed, const uint8_t* W2_packed,
+                              const uint8_t* W1_scale, const uint8_t* W3_scale, const uint8_t* W2_scale,
+                              int T, int topk, int n_experts, int K_in, int hidden, int out_dim,
+                              float routed_scale, dsv4_bf16_t* out, int32_t* ids_out, float* weights_out,
+                              void* workspace, hipStream_t stream);
 
 /* EXTENSION (no reference counterpart; the reference has no prefill MoE path,
  * though the benchmark configuration asks for a 512-token prefill chunk): the
@@ -157,6 +207,15 @@ int mxfp4_moe_prefill(const dsv4_bf16_t* x,
                       const int32_t* ids, const float* weights, int T, int topk, int n_experts,
                       int K_in, int hidden, int out_dim, dsv4_bf16_t* out, void* workspace,
                       hipStream_t stream);
+
+/* EXTENSION (debug): out[n,k] = bf16( e2m1(W[n,k]) * 2^(S[n,k/32]-127) ) with
+ * the decode of the prefill GEMMs (the conversion applies the block scale),
+ * for the bit-exact check against runtime/mxfp4_loader.py:272-309 (byte 0 ->
+ * 2^-127, 0xFF -> 0 as the decode path). W [N, K/2] and out [N, K] contiguous
+ * and 16-byte aligned, S [N, K/32]. Returns 0; -1 K%32; -3 bad operand; -4
+ * launch failure. */
+int mxfp4_moe_prefill_dequant_bf16(const uint8_t* W_packed, const uint8_t* W_scale, int K, int N,
+                                   dsv4_bf16_t* out, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* libmxfp4_gemv.so                                                          */

@@ -38,6 +38,9 @@ def lib() -> ctypes.CDLL:
         L.mxo_grouped_gemv.argtypes = [P] * 8 + [I] * 4 + [P]
         L.mxo_rmsnorm_residual.argtypes = [P, P, P, I, I, F, P, P]
         L.mxo_rmsnorm.argtypes = [P, P, I, I, F, P]
+        L.mxo_router_logits.argtypes = [P, I, P, I, I, P]
+        L.mxo_route_sqrt_softplus.argtypes = [P, I, I, F, P, P]
+        L.mxo_route_sqrt_softplus.restype = I
         _LIB = L
     return _LIB
 
@@ -114,3 +117,29 @@ def rmsnorm(x, w, eps: float = 1e-6) -> np.ndarray:
     y = np.empty_like(x2)
     lib().mxo_rmsnorm(_p(x2), _p(w), rows, H, eps, _p(y))
     return y
+
+
+def router_logits(x, w_gate) -> np.ndarray:
+    x = _c(np.atleast_2d(x), np.uint16)
+    w = _c(w_gate, np.uint16)
+    T, K = x.shape
+    N = w.shape[0]
+    out = np.empty((T, N), dtype=np.float32)
+    lib().mxo_router_logits(_p(x), T, _p(w), N, K, _p(out))
+    return out
+
+
+def route_sqrt_softplus(logits, topk: int, routed_scale: float = 1.5):
+    """Per row: (ids, weights, number of picks that were numbers)."""
+    l = _c(np.atleast_2d(logits), np.float32)
+    T, n = l.shape
+    ids = np.empty((T, topk), dtype=np.int32)
+    w = np.empty((T, topk), dtype=np.float32)
+    found = np.empty(T, dtype=np.int32)
+    for t in range(T):
+        row = _c(l[t], np.float32)
+        it = np.empty(topk, dtype=np.int32)
+        wt = np.empty(topk, dtype=np.float32)
+        found[t] = lib().mxo_route_sqrt_softplus(_p(row), n, topk, ctypes.c_float(routed_scale), _p(it), _p(wt))
+        ids[t], w[t] = it, wt
+    return ids, w, found

@@ -315,6 +315,63 @@ def route_sigmoid_topk(logits, topk: int):
         return ids, (s / s.sum(axis=1, keepdims=True)).astype(np.float32)
 
 
+def sqrt_softplus(logits) -> np.ndarray:
+    """The reference router's score s = sqrt(softplus(l)) in fp32, with
+    softplus(l) = max(l, 0) + log1p(exp(-|l|))
+    (kernel/cpp-engine-mxfp4/routed.cu:156-164; runtime/dsv4_engine_mxfp4.py:366
+    takes torch.sqrt(F.softplus(gate))).
+
+    Pinned: tests compare with torch.nn.functional.softplus + torch.sqrt in
+    fp32 (within 2 ulp) and with fp64 closed forms: s(0) = sqrt(ln 2),
+    s(l) = sqrt(l) for large l, s(-inf) = 0, s(+inf) = inf, s(NaN) = NaN."""
+    l = np.asarray(logits, dtype=np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        sp = (np.maximum(l, np.float32(0)) + np.log1p(np.exp(-np.abs(l)))).astype(np.float32)
+        return np.sqrt(sp).astype(np.float32)
+
+
+def route_sqrt_softplus_topk(logits, topk: int, routed_scale: float = 1.5):
+    """The reference router's selection and weights for each row of logits
+    (kernel/cpp-engine-mxfp4/routed.cu:169-208, runtime/dsv4_engine_mxfp4.py:
+    363-370): the top-k scores s = sqrt_softplus(l), descending, the first
+    maximum winning ties (the lower expert index); a NaN score is never above
+    a number. Weights (s_k / (sum_k' s_k' + 1e-20f)) * scale evaluated in
+    double with the sum in pick order, rounded to float32 (routed.cu:201-206;
+    the Python engine rounds them further to bf16).
+
+    Pinned: ids against torch.topk on distinct scores and against brute-force
+    first-maximum selection on ties; weights against closed forms (their sum
+    is scale * S / (S + 1e-20), their ratios are the score ratios)."""
+    s = sqrt_softplus(np.atleast_2d(logits))
+    key = np.where(np.isnan(s), -np.inf, s.astype(np.float64))
+    ids = np.argsort(-key, axis=1, kind="stable")[:, :topk].astype(np.int32)
+    sel = np.take_along_axis(s, ids, axis=1)
+    scale = float(np.float32(routed_scale))
+    eps = float(np.float32(1e-20))
+    w = np.empty(sel.shape, dtype=np.float32)
+    for t in range(sel.shape[0]):
+        total = 0.0
+        for k in range(topk):
+            total += float(sel[t, k])
+        denom = total + eps
+        for k in range(topk):
+            w[t, k] = np.float32((float(sel[t, k]) / denom) * scale)
+    return ids, w
+
+
+def router_logits(x, w_gate) -> np.ndarray:
+    """logits[t, n] = sum_k W_gate[n, k] * x[t, k] over bf16 operands
+    (kernel/cpp-engine-mxfp4/routed.cu:124-153), summed in fp64 and rounded
+    once to fp32. The reference and the device sum in fp32 in their own
+    orders, so they differ from this by a few ulps of sum_k |W x|.
+
+    Pinned: tests check it against the fp64 scalar C oracle on small shapes
+    and a one-hot x selecting a column of W_gate exactly."""
+    xf = bf16_to_f32(np.atleast_2d(x)).astype(np.float64)
+    wf = bf16_to_f32(w_gate).astype(np.float64)
+    return (xf @ wf.T).astype(np.float32)
+
+
 # ---------------------------------------------------------------- RMSNorm ---
 
 

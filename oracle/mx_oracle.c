@@ -16,6 +16,7 @@
  *   FP8 dequant          runtime/dsv4_engine_mxfp4.py:531-553
  *   routed SwiGLU        kernel/mxfp4-routed/mxfp4_grouped_gemv.cu:143-289
  *   fused RMSNorm        kernel/rmsnorm-fuse/rmsnorm_fuse.cu:110-157
+ *   router GEMV + scores kernel/cpp-engine-mxfp4/routed.cu:124-208
  */
 #include <math.h>
 #include <stdint.h>
@@ -171,4 +172,53 @@ void mxo_rmsnorm(const uint16_t* x, const uint16_t* w, int rows, int H, float ep
             y[(size_t)i * H + h] = mxo_bf16_rne((float)(v * rms));
         }
     }
+}
+
+/* Router gate logits in fp64: logits[t, n] = sum_k W[n, k] x[t, k] (bf16
+ * operands), rounded once to float. */
+void mxo_router_logits(const uint16_t* x, int T, const uint16_t* W, int N, int K, float* logits) {
+    for (int t = 0; t < T; ++t)
+        for (int n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k)
+                acc += (double)mxo_bf16_f32(W[(size_t)n * K + k]) * (double)mxo_bf16_f32(x[(size_t)t * K + k]);
+            logits[(size_t)t * N + n] = (float)acc;
+        }
+}
+
+/* The reference router's selection for one row of n logits: scores
+ * s = sqrtf(max(l, 0) + log1pf(expf(-|l|))); `topk` selection passes, each
+ * taking the first strictly larger untaken score (so ties go to the lower
+ * index and NaN is never taken while a number is left; with none left the
+ * pass takes the lowest untaken index); weights (s / (sum + 1e-20f)) * scale
+ * in double, sum in pick order. Returns the number of passes that found a
+ * number. */
+int mxo_route_sqrt_softplus(const float* logits, int n, int topk, float scale, int* ids, float* w) {
+    float* s = (float*)malloc((size_t)n * sizeof(float));
+    char* taken = (char*)calloc((size_t)n, 1);
+    for (int i = 0; i < n; ++i) {
+        float l = logits[i];
+        float sp = fmaxf(l, 0.0f) + log1pf(expf(-fabsf(l)));
+        s[i] = sqrtf(sp);
+    }
+    int found = 0;
+    for (int k = 0; k < topk; ++k) {
+        int best = -1;
+        float bv = -INFINITY;
+        for (int i = 0; i < n; ++i)
+            if (!taken[i] && s[i] > bv) { bv = s[i]; best = i; }
+        if (best >= 0) ++found;
+        else
+            for (int i = 0; i < n && best < 0; ++i)
+                if (!taken[i]) best = i;
+        ids[k] = best;
+        taken[best] = 1;
+    }
+    double sum = 0.0;
+    for (int k = 0; k < topk; ++k) sum += (double)s[ids[k]];
+    double denom = sum + (double)1e-20f;
+    for (int k = 0; k < topk; ++k) w[k] = (float)(((double)s[ids[k]] / denom) * (double)scale);
+    free(s);
+    free(taken);
+    return found;
 }

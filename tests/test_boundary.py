@@ -20,7 +20,9 @@ LIBS = {
         "mxfp4_grouped_gemv_topk", "mxfp4_grouped_workspace_bytes",
         "mxfp4_moe_route_sigmoid_topk", "mxfp4_moe_workspace_bytes", "mxfp4_moe_grouped_gemv",
         "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer",
-        "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill"],
+        "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill", "mxfp4_moe_prefill_dequant_bf16",
+        "mxfp4_moe_route_topk", "mxfp4_moe_router_logits", "mxfp4_moe_dispatch_workspace_bytes",
+        "mxfp4_moe_routed_dispatch"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
                                       "fp8_e4m3_swiglu_gemv", "fp8_e4m3_rmsnorm_gemv", "fp8_e4m3_dequant_bf16"],
@@ -139,6 +141,53 @@ def test_moe_validation_codes():
     wb.argtypes = [ctypes.c_int] * 4
     assert wb(16, 8, 256, 2048) >= 16 * 8 * 2048 * 2
     assert wb(0, 8, 256, 2048) == 0
+
+
+def test_router_and_dispatch_validation_codes():
+    lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
+    P, I = ctypes.c_void_p, ctypes.c_int
+    rt = lib.mxfp4_moe_route_topk
+    rt.restype = I
+    rt.argtypes = [P, I, I, I, I, ctypes.c_float, P, P, P]
+    assert rt(N, 1, 256, 6, 2, 1.5, N, N, N) == -1      # unknown score mode
+    assert rt(N, 1, 256, 6, -1, 1.5, N, N, N) == -1
+    assert rt(N, 0, 256, 6, 1, 1.5, N, N, N) == -1      # T < 1
+    assert rt(N, 1, 4, 6, 1, 1.5, N, N, N) == -1        # topk > n_experts
+    rl = lib.mxfp4_moe_router_logits
+    rl.restype = I
+    rl.argtypes = [P, P, I, I, I, P, P]
+    assert rl(N, N, 0, 256, 4096, N, N) == -1            # T < 1
+    assert rl(N, N, 65, 256, 4096, N, N) == -1           # T > 64
+    assert rl(N, N, 1, 1025, 4096, N, N) == -1           # n_experts > 1024
+    assert rl(N, N, 1, 256, 4100, N, N) == -1            # K % 8
+    assert rl(N, N, 1, 256, 8200, N, N) == -1            # K > 8192
+    assert rl(ctypes.c_void_p(8), N, 1, 256, 4096, N, N) == -3  # unaligned x
+    ws = lib.mxfp4_moe_dispatch_workspace_bytes
+    ws.restype = ctypes.c_size_t
+    ws.argtypes = [I] * 4
+    wm = lib.mxfp4_moe_workspace_bytes
+    wm.restype = ctypes.c_size_t
+    wm.argtypes = [I] * 4
+    assert ws(1, 6, 256, 2048) >= wm(1, 6, 256, 2048) + 256 * 4
+    assert ws(0, 6, 256, 2048) == 0
+    d = lib.mxfp4_moe_routed_dispatch
+    d.restype = I
+    d.argtypes = [P] * 8 + [I] * 6 + [ctypes.c_float] + [P] * 5
+
+    def call(T, k, E, K, H, O):
+        return d(*([N] * 8), T, k, E, K, H, O, 1.5, N, N, N, N, N)
+
+    assert call(1, 6, 256, 4095, 2048, 4096) == -1
+    assert call(1, 6, 256, 4096, 2047, 4096) == -2
+    assert call(1, 6, 256, 8192, 2048, 4096) == -3
+    assert call(1, 300, 256, 4096, 2048, 4096) == -4
+    assert call(1, 8, 4, 4096, 2048, 4096) == -4          # topk > n_experts
+    assert call(1, 6, 256, 4096, 2048, 4096) == -3        # null operands
+    pd = lib.mxfp4_moe_prefill_dequant_bf16
+    pd.restype = I
+    pd.argtypes = [P, P, I, I, P, P]
+    assert pd(N, N, 100, 4, N, N) == -1
+    assert pd(N, N, 128, 4, N, N) == -3
 
 
 def test_prefill_validation_codes():

@@ -414,16 +414,19 @@ def test_moe_duplicate_and_out_of_range_ids(device):
     assert_close(host_bits(out1), host_bits(out)[:1], "duplicate merge", cos_tol=0.99999)
 
 
+@pytest.mark.parametrize("K", [2048, 4096])
 @pytest.mark.parametrize("ids_row", [[3, 5, 1, 7, 12, 0, 9, 14], [3, 3, 5, 15, 3, 8, 8, 1],
                                      [-1, 2, 16, 2, 1000, -7, 4, 2], [6, 6, 6, 6, 6, 6, 6, 6]],
                          ids=["distinct", "duplicates", "invalid-and-duplicates", "one-expert"])
-def test_moe_one_token_ids_path(device, ids_row):
+def test_moe_one_token_ids_path(device, ids_row, K):
     """At T = 1 mxfp4_moe_grouped_gemv forms the routing inside stage A (two
     launches). Its slots (distinct in-range ids, ascending, summed weights of
     repeated listings) and results must equal the routing kernel's path
-    (build_routing + swiglu + down) bit for bit, and the oracle."""
-    E, K, H, O, topk = 16, 2048, 256, 256, 8
-    announce(f"mxfp4_moe_grouped_gemv T=1 ids path {ids_row}")
+    (build_routing + swiglu + down) bit for bit, and the oracle. K = 2048 and
+    4096 are the one-token kernel's two instantiations (one or two MX blocks
+    per lane per row); 4096 is the configuration's."""
+    E, H, O, topk = 16, 256, 256, 8
+    announce(f"mxfp4_moe_grouped_gemv T=1 ids path K={K} {ids_row}")
     W1p, W1s = synth.mxfp4_weight(8400, H, K, E)
     W3p, W3s = synth.mxfp4_weight(8404, H, K, E)
     W2p, W2s = synth.mxfp4_weight(8408, O, H, E)
