@@ -33,6 +33,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "dsv4_device.h"
 #include "dsv4_kernels.h"
@@ -2100,15 +2101,23 @@ extern "C" int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale,
     return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
 }
 
-extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_packed,
-                                      const uint8_t* W3_packed, const uint8_t* W2_packed,
-                                      const uint8_t* W1_scale, const uint8_t* W3_scale,
-                                      const uint8_t* W2_scale, const int32_t* ids,
-                                      const float* weights, int T, int topk, int n_experts,
-                                      int K_in, int hidden, int out_dim, dsv4_bf16_t* out,
-                                      void* workspace, hipStream_t stream) {
-    int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
-    if (v != 0) return v;
+// Device scratch of mxfp4_moe_grouped_gemv_noalloc: the routing tables and
+// the SwiGLU intermediate that the workspace holds otherwise (4 MiB: T*topk
+// rows of hidden bf16 plus the tables). Each GPU the library runs on holds its
+// own copy until the process ends. Host code uses the per-device address from
+// hipGetSymbolAddress, never the array's name.
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+// mxfp4_moe_grouped_gemv after validation, on the given workspace.
+int moe_grouped_impl(const dsv4_bf16_t* x, const uint8_t* W1_packed, const uint8_t* W3_packed,
+                     const uint8_t* W2_packed, const uint8_t* W1_scale, const uint8_t* W3_scale,
+                     const uint8_t* W2_scale, const int32_t* ids, const float* weights, int T, int topk,
+                     int n_experts, int K_in, int hidden, int out_dim, dsv4_bf16_t* out, void* workspace,
+                     hipStream_t stream) {
+    int v;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     if (T == 1) {
         // One token: stage A forms the slots from the ids itself (two
@@ -2132,6 +2141,70 @@ extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_pa
     v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
     if (v != 0) return v;
     return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up on its first use.
+int scratch_for_current_device(void** ptr) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        std::fprintf(stderr, "mxfp4 moe noalloc: no current device\n");
+        return -9;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            std::fprintf(stderr, "mxfp4 moe noalloc: hipGetSymbolAddress failed: %s\n", hipGetErrorString(e));
+            return -9;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_packed,
+                                      const uint8_t* W3_packed, const uint8_t* W2_packed,
+                                      const uint8_t* W1_scale, const uint8_t* W3_scale,
+                                      const uint8_t* W2_scale, const int32_t* ids,
+                                      const float* weights, int T, int topk, int n_experts,
+                                      int K_in, int hidden, int out_dim, dsv4_bf16_t* out,
+                                      void* workspace, hipStream_t stream) {
+    const int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
+    if (v != 0) return v;
+    return moe_grouped_impl(x, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale, ids, weights, T,
+                            topk, n_experts, K_in, hidden, out_dim, out, workspace, stream);
+}
+
+extern "C" int mxfp4_moe_grouped_gemv_noalloc(const dsv4_bf16_t* x, const uint8_t* W1_packed,
+                                              const uint8_t* W3_packed, const uint8_t* W2_packed,
+                                              const uint8_t* W1_scale, const uint8_t* W3_scale,
+                                              const uint8_t* W2_scale, const int32_t* ids,
+                                              const float* weights, int T, int topk, int n_experts,
+                                              int K_in, int hidden, int out_dim, dsv4_bf16_t* out,
+                                              hipStream_t stream) {
+    const int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
+    if (v != 0) return v;
+    const size_t need = moe_layout(T, topk, n_experts, hidden).total;
+    if (need > kScratchBytes) {
+        std::fprintf(stderr,
+                     "mxfp4_moe_grouped_gemv_noalloc: T=%d topk=%d hidden=%d needs %zu bytes of scratch, "
+                     "more than the %zu the library holds; use mxfp4_moe_grouped_gemv with a workspace\n",
+                     T, topk, hidden, need, kScratchBytes);
+        return -8;
+    }
+    void* ws = nullptr;
+    const int r = scratch_for_current_device(&ws);
+    if (r != 0) return r;
+    return moe_grouped_impl(x, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale, ids, weights, T,
+                            topk, n_experts, K_in, hidden, out_dim, out, ws, stream);
 }
 
 extern "C" int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,

@@ -80,6 +80,8 @@ def _load_lib() -> ctypes.CDLL:
     lib.mxfp4_moe_router_logits.argtypes = [_c_void_p] * 2 + [_c_int] * 3 + [_c_void_p] * 2
     lib.mxfp4_moe_dispatch_workspace_bytes.restype = _c_size_t
     lib.mxfp4_moe_dispatch_workspace_bytes.argtypes = [_c_int] * 4
+    lib.mxfp4_moe_grouped_gemv_noalloc.restype = _c_int
+    lib.mxfp4_moe_grouped_gemv_noalloc.argtypes = ([_c_void_p] * 9 + [_c_int] * 6 + [_c_void_p] * 2)
     lib.mxfp4_moe_routed_dispatch.restype = _c_int
     lib.mxfp4_moe_routed_dispatch.argtypes = ([_c_void_p] * 8 + [_c_int] * 6 + [ctypes.c_float] +
                                              [_c_void_p] * 5)

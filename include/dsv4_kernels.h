@@ -135,6 +135,29 @@ int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x,
                            int K_in, int hidden, int out_dim,
                            dsv4_bf16_t* out, void* workspace, hipStream_t stream);
 
+/* EXTENSION, no counterpart in the reference: mxfp4_moe_grouped_gemv without a
+ * workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The routing tables and the SwiGLU intermediate live in a 4 MiB
+ * device array that the library holds on each GPU it runs on (of the current
+ * device, hipGetDevice; `stream` must belong to it) until the process ends;
+ * the call allocates nothing. Calls that overlap on one GPU (two streams, two
+ * threads) share that array and race; calls in order on one stream are safe,
+ * and nothing carries over from one call to the next. Same arguments, results
+ * (the same bits) and return codes as mxfp4_moe_grouped_gemv, plus -8 when
+ * mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden) exceeds 4 MiB
+ * (e.g. T*topk*hidden*2 above about 4.1 million bytes) and -9 when the device
+ * array cannot be located. */
+int mxfp4_moe_grouped_gemv_noalloc(const dsv4_bf16_t* x,
+                                   const uint8_t* W1_packed, const uint8_t* W3_packed,
+                                   const uint8_t* W2_packed,
+                                   const uint8_t* W1_scale, const uint8_t* W3_scale,
+                                   const uint8_t* W2_scale,
+                                   const int32_t* ids, const float* weights,
+                                   int T, int topk, int n_experts,
+                                   int K_in, int hidden, int out_dim,
+                                   dsv4_bf16_t* out, hipStream_t stream);
+
 /* EXTENSION: the three launches of mxfp4_moe_grouped_gemv as separate entry
  * points (same arguments and workspace), for callers that schedule or overlap
  * the projections themselves and for per-launch timing:

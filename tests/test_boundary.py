@@ -22,7 +22,7 @@ LIBS = {
         "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer",
         "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill", "mxfp4_moe_prefill_dequant_bf16",
         "mxfp4_moe_route_topk", "mxfp4_moe_router_logits", "mxfp4_moe_dispatch_workspace_bytes",
-        "mxfp4_moe_routed_dispatch"],
+        "mxfp4_moe_routed_dispatch", "mxfp4_moe_grouped_gemv_noalloc"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
                                       "fp8_e4m3_swiglu_gemv", "fp8_e4m3_rmsnorm_gemv", "fp8_e4m3_dequant_bf16"],
@@ -141,6 +141,29 @@ def test_moe_validation_codes():
     wb.argtypes = [ctypes.c_int] * 4
     assert wb(16, 8, 256, 2048) >= 16 * 8 * 2048 * 2
     assert wb(0, 8, 256, 2048) == 0
+
+
+def test_noalloc_validation_codes():
+    """The no-allocation entry validates like mxfp4_moe_grouped_gemv and rejects
+    shapes whose tables and intermediate exceed its 4 MiB device array, all
+    before any HIP call."""
+    lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
+    f = lib.mxfp4_moe_grouped_gemv_noalloc
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 9 + [ctypes.c_int] * 6 + [ctypes.c_void_p] * 2
+
+    def call(T, k, E, K, H, O):
+        return f(N, N, N, N, N, N, N, N, N, T, k, E, K, H, O, N, N)
+
+    assert call(1, 8, 256, 4095, 2048, 4096) == -1
+    assert call(1, 8, 256, 4096, 2047, 4096) == -2
+    assert call(65, 8, 256, 4096, 2048, 4096) == -4
+    assert call(64, 16, 256, 4096, 4096, 4096) == -8     # 1024 rows x 8 KiB of intermediate
+    assert call(64, 16, 256, 4096, 2048, 4096) == -8     # 4 MiB + tables
+    wb = lib.mxfp4_moe_workspace_bytes
+    wb.restype = ctypes.c_size_t
+    wb.argtypes = [ctypes.c_int] * 4
+    assert wb(16, 8, 256, 2048) <= 4 << 20                 # the configuration's T <= 16 fits
 
 
 def test_router_and_dispatch_validation_codes():
