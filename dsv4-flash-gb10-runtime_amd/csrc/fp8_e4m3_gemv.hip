@@ -157,45 +157,65 @@ __device__ __forceinline__ float swiglu_clamp(float v, float limit) {
     return limit > 0.f ? fminf(fmaxf(v, -limit), limit) : v;
 }
 
-// Tile kernel for K in {2048, 4096} with 16-byte aligned rows and
-// activations (the MLA projection shapes). A workgroup of 256 threads owns
+// Tile kernels for K in {1024, 2048, 4096, 8192} with 16-byte aligned rows
+// and activations (the MLA projection shapes). A workgroup of 256 threads owns
 // R = C*256/KC rows (KC = K/16 chunks per row); thread t takes the chunks
-// t, t+256, ..., t+256*(C-1) of the workgroup's [R, KC] chunk grid, so all of
-// its chunks share one k-slice (k = 16*(t % KC)) and every wave instruction
-// reads 1 KiB of a single row. Each thread issues its activation slice for all
-// TT tokens first (16 bf16 per token), then its C weight chunks (of each of
-// the MAT matrices) and their tile-scale bytes, all unconditional (rows
-// clamped, tokens past T clamped to T-1 and not stored), so everything is in
-// flight after one issue pass. Per-wave partials (C x TT values per matrix,
-// one butterfly per matrix) meet in LDS and are added in a fixed order:
-// deterministic, and with MAT = 2 each matrix's sums are the bits the
-// single-matrix kernel produces. blockIdx.y is the group (GroupView).
+// t, t+256, ..., t+256*(C-1) of the workgroup's [R, KC] chunk grid, so every
+// wave instruction reads 1 KiB of a single row, and its chunks use KS =
+// max(1, KC/256) k-slices (one for K <= 4096, two for K = 8192). Each thread
+// issues its activation slices for the first TT tokens first (16 bf16 per
+// token and slice), then its C weight chunks (of each of the MAT matrices)
+// and their tile-scale bytes, all unconditional (rows clamped, tokens past T
+// clamped to T-1 and not stored), so everything is in flight after one issue
+// pass. The weights stay in registers while the tokens are taken TT at a
+// time: no weight byte is read twice, whatever T. Per-wave partials (C x TT
+// values per matrix, one butterfly per matrix) meet in LDS and are added in a
+// fixed order: deterministic, and with MAT = 2 each matrix's sums are the
+// bits the single-matrix kernel produces.
 template <int C, int TT, int KC, int MAT>
-__global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a, const SwigluArgs sw) {
-    constexpr int kRowsWG = C * 256 / KC;
-    constexpr int kVals = C * TT;
-    __shared__ float part[kWaves][MAT][C][TT];
+struct TileShape {
+    static constexpr int kRowsWG = C * 256 / KC;
+    static constexpr int KS = KC > 256 ? KC / 256 : 1;
+    static constexpr int kVals = C * TT;
+    static_assert(256 % KC == 0 || KC % 256 == 0, "chunks per row must divide or be a multiple of 256");
+    static_assert(C % KS == 0, "every thread takes whole rows of slices");
+};
+
+// The body shared by the single-matrix, grouped and multi-matrix launches:
+// workgroup `blk` of the matrix described by `a` and `gv`.
+template <int C, int TT, int KC, int MAT>
+__device__ __forceinline__ void fp8_tile_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
+                                              int blk, float (*part)[MAT][C][TT]) {
+    using S = TileShape<C, TT, KC, MAT>;
+    constexpr int kRowsWG = S::kRowsWG, KS = S::KS, kVals = S::kVals;
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int n0 = blockIdx.x * kRowsWG;
-    const int k = 16 * (t % KC);
-    const GroupView gv = group_view(a);
+    const int n0 = blk * kRowsWG;
+    const int kb = 16 * (t % (KC < 256 ? KC : 256));   // k of slice 0; slice s adds 4096*s
 
-    uint32_t xp[TT][8];
+    uint32_t xp[TT][KS][8];
+    auto load_x = [&](int tok0) {
 #pragma unroll
-    for (int tok = 0; tok < TT; ++tok) {
-        const u32x4* s4 = reinterpret_cast<const u32x4*>(gv.x + (int64_t)min(tok, a.T - 1) * a.xstride + k);
-        const u32x4 v0 = s4[0], v1 = s4[1];
-        xp[tok][0] = v0[0]; xp[tok][1] = v0[1]; xp[tok][2] = v0[2]; xp[tok][3] = v0[3];
-        xp[tok][4] = v1[0]; xp[tok][5] = v1[1]; xp[tok][6] = v1[2]; xp[tok][7] = v1[3];
-    }
+        for (int tok = 0; tok < TT; ++tok) {
+            const uint16_t* xr = gv.x + (int64_t)min(tok0 + tok, a.T - 1) * a.xstride;
+#pragma unroll
+            for (int q = 0; q < KS; ++q) {
+                const u32x4* s4 = reinterpret_cast<const u32x4*>(xr + kb + 4096 * q);
+                const u32x4 v0 = s4[0], v1 = s4[1];
+                xp[tok][q][0] = v0[0]; xp[tok][q][1] = v0[1]; xp[tok][q][2] = v0[2]; xp[tok][q][3] = v0[3];
+                xp[tok][q][4] = v1[0]; xp[tok][q][5] = v1[1]; xp[tok][q][6] = v1[2]; xp[tok][q][7] = v1[3];
+            }
+        }
+    };
+    load_x(0);
     __builtin_amdgcn_sched_barrier(0);  // activation loads first
     u32x4 w[MAT][C];
     uint32_t sb[MAT][C];
 #pragma unroll
     for (int i = 0; i < C; ++i) {
         const int64_t gn = gv.row0 + min(n0 + (t + 256 * i) / KC, a.N - 1);
+        const int k = kb + 4096 * (i % KS);
         w[0][i] = ld16_stream(a.w + gn * a.wrow + k);
         sb[0][i] = a.s[(gn / kTile) * a.srow + k / kTile];
         if constexpr (MAT == 2) {
@@ -203,46 +223,94 @@ __global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a, con
             sb[1][i] = sw.s3[(gn / kTile) * a.srow + k / kTile];
         }
     }
-#pragma unroll
-    for (int m = 0; m < MAT; ++m) {
-        float acc[kVals];
-#pragma unroll
-        for (int i = 0; i < C; ++i) {
-            const float sc = e8m0_to_f32(sb[m][i]);
-#pragma unroll
-            for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[m][i], xp[tok]) * sc;
+    for (int tok0 = 0; tok0 < a.T; tok0 += TT) {
+        if (tok0 > 0) {
+            __syncthreads();    // the previous group's partials are consumed
+            load_x(tok0);
         }
-        wave_reduce_n<kVals>(acc, lane);
-        const int v = reduced_index<kVals>(lane);
-        if (reduced_owner<kVals>(lane)) part[wave][m][v / TT][v % TT] = acc[0];
-    }
-    __syncthreads();
-    for (int o = t; o < kRowsWG * TT; o += 256) {
-        const int r = o / TT;
-        const int tok = o % TT;
-        if (tok >= a.T || n0 + r >= a.N) continue;
-        float sum[MAT];
 #pragma unroll
         for (int m = 0; m < MAT; ++m) {
-            sum[m] = 0.f;
+            float acc[kVals];
 #pragma unroll
-            for (int w2 = 0; w2 < kWaves; ++w2) {
+            for (int i = 0; i < C; ++i) {
+                const float sc = e8m0_to_f32(sb[m][i]);
 #pragma unroll
-                for (int i = 0; i < C; ++i)
-                    if ((64 * w2 + 256 * i) / KC == r) sum[m] += part[w2][m][i][tok];
+                for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[m][i], xp[tok][i % KS]) * sc;
             }
+            wave_reduce_n<kVals>(acc, lane);
+            const int v = reduced_index<kVals>(lane);
+            if (reduced_owner<kVals>(lane)) part[wave][m][v / TT][v % TT] = acc[0];
         }
-        uint16_t out;
-        if constexpr (MAT == 2) {
-            const float g = swiglu_clamp(bf16_bits_to_f32(f32_to_bf16_bits(sum[0])), sw.limit);
-            const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(sum[1]));
-            const float u = sw.clamp_up ? swiglu_clamp(u0, sw.limit) : u0;
-            out = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
-        } else {
-            out = f32_to_bf16_bits(sum[0]);
+        __syncthreads();
+        for (int o = t; o < kRowsWG * TT; o += 256) {
+            const int r = o / TT;
+            const int tok = o % TT;
+            if (tok0 + tok >= a.T || n0 + r >= a.N) continue;
+            float sum[MAT];
+#pragma unroll
+            for (int m = 0; m < MAT; ++m) {
+                sum[m] = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < kWaves; ++w2) {
+#pragma unroll
+                    for (int i = 0; i < C; ++i)
+                        if ((64 * w2 + 256 * i) / KC == r) sum[m] += part[w2][m][i][tok];
+                }
+            }
+            uint16_t out;
+            if constexpr (MAT == 2) {
+                const float g = swiglu_clamp(bf16_bits_to_f32(f32_to_bf16_bits(sum[0])), sw.limit);
+                const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(sum[1]));
+                const float u = sw.clamp_up ? swiglu_clamp(u0, sw.limit) : u0;
+                out = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+            } else {
+                out = f32_to_bf16_bits(sum[0]);
+            }
+            gv.y[(int64_t)(tok0 + tok) * a.ystride + n0 + r] = out;
         }
-        gv.y[(int64_t)tok * a.ystride + n0 + r] = out;
     }
+}
+
+// One matrix, or G row groups of one matrix (blockIdx.y, GroupView).
+template <int C, int TT, int KC, int MAT>
+__global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a, const SwigluArgs sw) {
+    __shared__ float part[kWaves][MAT][C][TT];
+    fp8_tile_body<C, TT, KC, MAT>(a, sw, group_view(a), blockIdx.x, part);
+}
+
+// Several matrices that read the same activation (the pointer table of
+// fp8_e4m3_gemv_multi): matrix m owns workgroups first[m] .. first[m+1]-1.
+constexpr int kMaxMulti = 8;
+
+struct MultiArgs {
+    Fp8Args base;                       // x, xstride, K, T (w, s, N, strides, y per matrix below)
+    int n_mats;
+    int first[kMaxMulti + 1];
+    const uint8_t* w[kMaxMulti];
+    const uint8_t* s[kMaxMulti];
+    int N[kMaxMulti];
+    int64_t wrow[kMaxMulti];
+    int64_t srow[kMaxMulti];
+    uint16_t* y[kMaxMulti];
+    int64_t ystride[kMaxMulti];
+};
+
+template <int C, int TT, int KC>
+__global__ __launch_bounds__(256) void fp8_gemv_multi_kernel(const MultiArgs ma) {
+    __shared__ float part[kWaves][1][C][TT];
+    int m = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxMulti; ++j) m += (j < ma.n_mats && (int)blockIdx.x >= ma.first[j]) ? 1 : 0;
+    Fp8Args a = ma.base;
+    a.w = ma.w[m];
+    a.s = ma.s[m];
+    a.N = ma.N[m];
+    a.wrow = ma.wrow[m];
+    a.srow = ma.srow[m];
+    a.y = ma.y[m];
+    a.ystride = ma.ystride[m];
+    const GroupView gv{a.x, a.y, 0};
+    fp8_tile_body<C, TT, KC, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part);
 }
 
 // RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
@@ -455,28 +523,78 @@ int validate(int K, int N) {
     return 0;
 }
 
+bool tile_k(int K) { return K == 1024 || K == 2048 || K == 4096 || K == 8192; }
+
 bool tile_ok(const Fp8Args& a) {
     return aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) && (a.T == 1 || a.xstride % 8 == 0) &&
-           (a.xgroup % 8 == 0) && (a.K == 2048 || a.K == 4096);
+           (a.xgroup % 8 == 0) && tile_k(a.K);
 }
 
-// G groups (grid.y). MAT = 2: the fused SwiGLU (tile shapes only, T <= 8
-// per launch).
+// Rows per workgroup of the tile kernels: four chunks per thread.
+int tile_rows(int K) { return 4 * 256 / (K / 16); }
+
+// Tokens per group: all of them up to 16 (8 with two matrices), at most 4 per
+// group with two k-slices per thread (K = 8192), which hold twice the
+// activation registers.
+int tile_tt(int T, int K, int MAT) {
+    const int cap = K > 4096 ? 4 : (MAT == 2 ? 8 : 16);
+    const int tt = T == 1 ? 1 : (T == 2 ? 2 : (T <= 4 ? 4 : (T <= 8 ? 8 : 16)));
+    return tt < cap ? tt : cap;
+}
+
+// Launch the tile kernel for TT tokens per group at the row length K (K = 8192
+// only with TT <= 4: tile_tt never asks for more there).
+template <int TT, int MAT>
+void launch_tile_tt(const Fp8Args& a, const SwigluArgs& sw, dim3 grid, hipStream_t stream) {
+    switch (a.K) {
+        case 1024: hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 64, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 128, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 256, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        default:
+            if constexpr (TT <= 4)
+                hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 512, MAT>), grid, dim3(256), 0, stream, a, sw);
+            break;
+    }
+}
+
+template <int TT>
+void launch_multi_tt(const MultiArgs& ma, dim3 grid, hipStream_t stream) {
+    switch (ma.base.K) {
+        case 1024: hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 64>), grid, dim3(256), 0, stream, ma); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 128>), grid, dim3(256), 0, stream, ma); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 256>), grid, dim3(256), 0, stream, ma); break;
+        default:
+            if constexpr (TT <= 4)
+                hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 512>), grid, dim3(256), 0, stream, ma);
+            break;
+    }
+}
+
+// G groups (grid.y). MAT = 2: the fused SwiGLU.
 template <int MAT>
 hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
-    // Four chunks per thread: 4 rows per workgroup at K = 4096, 8 at 2048.
-    const int KC = a.K / 16;
-    const int rows = 4 * 256 / KC;
-    const dim3 grid((unsigned)((a.N + rows - 1) / rows), (unsigned)G);
-#define DSV4_TILE(TTV)                                                                                          \
-    if (KC == 256) hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 256, MAT>), grid, dim3(256), 0, stream, a, sw); \
-    else hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TTV, 128, MAT>), grid, dim3(256), 0, stream, a, sw);
-    if (a.T == 1) { DSV4_TILE(1) }
-    else if (a.T == 2) { DSV4_TILE(2) }
-    else if (a.T <= 4) { DSV4_TILE(4) }
-    else if (a.T <= 8 || MAT == 2) { DSV4_TILE(8) }
-    else { DSV4_TILE(16) }
-#undef DSV4_TILE
+    const dim3 grid((unsigned)((a.N + tile_rows(a.K) - 1) / tile_rows(a.K)), (unsigned)G);
+    switch (tile_tt(a.T, a.K, MAT)) {
+        case 1: launch_tile_tt<1, MAT>(a, sw, grid, stream); break;
+        case 2: launch_tile_tt<2, MAT>(a, sw, grid, stream); break;
+        case 4: launch_tile_tt<4, MAT>(a, sw, grid, stream); break;
+        case 8: launch_tile_tt<8, MAT>(a, sw, grid, stream); break;
+        default:
+            if constexpr (MAT == 1) launch_tile_tt<16, MAT>(a, sw, grid, stream);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
+    const dim3 grid((unsigned)blocks);
+    switch (tile_tt(ma.base.T, ma.base.K, 1)) {
+        case 1: launch_multi_tt<1>(ma, grid, stream); break;
+        case 2: launch_multi_tt<2>(ma, grid, stream); break;
+        case 4: launch_multi_tt<4>(ma, grid, stream); break;
+        case 8: launch_multi_tt<8>(ma, grid, stream); break;
+        default: launch_multi_tt<16>(ma, grid, stream); break;
+    }
     return hipGetLastError();
 }
 
@@ -558,6 +676,74 @@ extern "C" int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride,
     return launch(a, G, stream);
 }
 
+extern "C" int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, int K, int T, int n_mats,
+                                   const uint8_t* const* W_fp8, const uint8_t* const* W_scale, const int* N,
+                                   const int64_t* weight_row_stride_bytes, const int64_t* scale_row_stride_bytes,
+                                   dsv4_bf16_t* const* y, const int64_t* y_row_stride, hipStream_t stream) {
+    if (n_mats < 1 || n_mats > kMaxMulti || !W_fp8 || !W_scale || !N || !weight_row_stride_bytes ||
+        !scale_row_stride_bytes || !y || !y_row_stride) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_multi: n_mats=%d outside [1, %d] or a null table\n", n_mats, kMaxMulti);
+        return -6;
+    }
+    for (int m = 0; m < n_mats; ++m) {
+        const int v = validate(K, N[m]);
+        if (v != 0) return v;
+    }
+    if (T < 1 || T > kMaxT) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_multi: T=%d outside [1, %d]\n", T, kMaxT);
+        return -5;
+    }
+    MultiArgs ma{};
+    ma.base = Fp8Args{reinterpret_cast<const uint16_t*>(x), x_row_stride, nullptr, nullptr, K, 0, T, 0, 0,
+                      nullptr, 0, 0, 0};
+    ma.n_mats = n_mats;
+    bool tile = true;
+    int blocks = 0;
+    for (int m = 0; m < n_mats; ++m) {
+        Fp8Args a = ma.base;
+        a.w = W_fp8[m];
+        a.s = W_scale[m];
+        a.N = N[m];
+        a.wrow = weight_row_stride_bytes[m];
+        a.srow = scale_row_stride_bytes[m];
+        a.y = reinterpret_cast<uint16_t*>(y[m]);
+        a.ystride = y_row_stride[m];
+        tile = tile && tile_ok(a);
+        ma.first[m] = blocks;
+        ma.w[m] = a.w;
+        ma.s[m] = a.s;
+        ma.N[m] = a.N;
+        ma.wrow[m] = a.wrow;
+        ma.srow[m] = a.srow;
+        ma.y[m] = a.y;
+        ma.ystride[m] = a.ystride;
+        blocks += (N[m] + tile_rows(K) - 1) / tile_rows(K);
+    }
+    ma.first[n_mats] = blocks;
+    if (!tile) {
+        // Shapes off the tile path: one launch per matrix.
+        for (int m = 0; m < n_mats; ++m) {
+            Fp8Args a = ma.base;
+            a.w = ma.w[m];
+            a.s = ma.s[m];
+            a.N = ma.N[m];
+            a.wrow = ma.wrow[m];
+            a.srow = ma.srow[m];
+            a.y = ma.y[m];
+            a.ystride = ma.ystride[m];
+            const int r = launch(a, 1, stream);
+            if (r != 0) return r;
+        }
+        return 0;
+    }
+    const hipError_t e = launch_multi(ma, blocks, stream);
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_multi launch failed: %s\n", hipGetErrorString(e));
+        return -4;
+    }
+    return 0;
+}
+
 extern "C" int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W1_fp8,
                                     const uint8_t* W1_scale, const uint8_t* W3_fp8, const uint8_t* W3_scale,
                                     int K, int N, int T, int64_t weight_row_stride_bytes,
@@ -573,8 +759,8 @@ extern "C" int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, 
               weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(act),
               act_row_stride, 0, 0};
     if (!tile_ok(a) || !aligned16(W3_fp8)) {
-        std::fprintf(stderr, "fp8_e4m3_swiglu_gemv: needs K in {2048, 4096} and 16-byte aligned x, W1, W3 "
-                             "and rows\n");
+        std::fprintf(stderr, "fp8_e4m3_swiglu_gemv: needs K in {1024, 2048, 4096, 8192} and 16-byte aligned x, "
+                             "W1, W3 and rows\n");
         return -6;
     }
     const SwigluArgs sw{W3_fp8, W3_scale, limit, clamp_up};
@@ -625,7 +811,8 @@ extern "C" int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* re
     }
     Fp8Args a{reinterpret_cast<const uint16_t*>(x), K, W_fp8, W_scale, K, N, T,
               weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y), N, 0, 0};
-    const bool ok = tile_ok(a) && norm_weight && x_norm && aligned16(norm_weight) && aligned16(x_norm) &&
+    const bool ok = tile_ok(a) && (K == 2048 || K == 4096) && norm_weight && x_norm && aligned16(norm_weight) &&
+                    aligned16(x_norm) &&
                     (!residual || (aligned16(residual) && new_residual && aligned16(new_residual)));
     if (!ok) {
         std::fprintf(stderr, "fp8_e4m3_rmsnorm_gemv: needs K in {2048, 4096}, 16-byte aligned operands, "

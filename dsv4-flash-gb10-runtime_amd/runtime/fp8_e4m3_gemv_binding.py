@@ -9,6 +9,9 @@ Differences, both extensions: N need not be a multiple of 128 (the reference
 raises for it), and x may be [T, K] with T <= 16, in which case one launch
 streams W once for all T tokens and y is [T, N].
 
+Extension: fp8_e4m3_gemv_multi([(W, S), ...], x) -> [y, ...]: several GEMVs
+on one activation in one launch.
+
 Extension (debug): fp8_e4m3_dequant(W_fp8, W_scale) -> [N, K] bf16.
 
 Errors: RuntimeError for device/dtype/shape problems and for a non-zero
@@ -51,6 +54,8 @@ def _load_lib() -> ctypes.CDLL:
         lib.fp8_e4m3_swiglu_gemv.restype = I
         lib.fp8_e4m3_rmsnorm_gemv.argtypes = [P, P, P, ctypes.c_float, P, P, I, I, I, L, L, P, P, P, P]
         lib.fp8_e4m3_rmsnorm_gemv.restype = I
+        lib.fp8_e4m3_gemv_multi.argtypes = [P, L, I, I, I] + [P] * 7 + [P]
+        lib.fp8_e4m3_gemv_multi.restype = I
         _LIB = lib
     return _LIB
 
@@ -160,6 +165,60 @@ def fp8_e4m3_gemv_grouped(
     if rc != 0:
         raise RuntimeError(f"fp8_e4m3_gemv_grouped returned {rc}")
     return out
+
+
+def fp8_e4m3_gemv_multi(
+    mats,
+    x: torch.Tensor,
+    outs=None,
+    stream: Optional[torch.cuda.Stream] = None,
+):
+    """Several GEMVs on one activation in one launch: mats is a list of
+    (W_fp8 [N_m, K], W_scale [ceil(N_m/128), K/128]) pairs (at most 8); x is
+    [K] or [T, K]; returns the list of y_m ([N_m] or [T, N_m]). wq_a and wkv on
+    the normalised row, kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:395-418."""
+    mats = list(mats)
+    if not 1 <= len(mats) <= 8:
+        raise RuntimeError(f"{len(mats)} matrices: between 1 and 8 are allowed")
+    if not x.is_cuda or x.dtype != torch.bfloat16:
+        raise RuntimeError("x must be a GPU bfloat16 tensor")
+    K = x.shape[-1]
+    T = 1 if x.dim() == 1 else x.shape[0]
+    if T > MAX_TOKENS:
+        raise RuntimeError(f"T={T} > {MAX_TOKENS}")
+    x = x.contiguous()
+    n = len(mats)
+    ws, ss, Ns, wst, sst, ys, yst = [], [], [], [], [], [], []
+    if outs is None:
+        outs = [None] * n
+    res = []
+    for (W, S), o in zip(mats, outs):
+        _check_w(W, S)
+        if W.shape[1] != K:
+            raise RuntimeError(f"W has K={W.shape[1]}, x has K={K}")
+        Nm = W.shape[0]
+        oshape = (Nm,) if x.dim() == 1 else (T, Nm)
+        if o is None:
+            o = torch.empty(oshape, dtype=torch.bfloat16, device=x.device)
+        elif tuple(o.shape) != oshape or o.dtype != torch.bfloat16 or not o.is_cuda or not o.is_contiguous():
+            raise RuntimeError(f"out must be a contiguous GPU bfloat16 {oshape} tensor")
+        ws.append(W.data_ptr())
+        ss.append(S.data_ptr())
+        Ns.append(Nm)
+        wst.append(W.stride(0))
+        sst.append(S.stride(0))
+        ys.append(o.data_ptr())
+        yst.append(Nm)
+        res.append(o)
+    PA = ctypes.c_void_p * n
+    IA = ctypes.c_int * n
+    LA = ctypes.c_int64 * n
+    rc = _load_lib().fp8_e4m3_gemv_multi(
+        _lib.vp(x), K, K, T, n, PA(*ws), PA(*ss), IA(*Ns), LA(*wst), LA(*sst), PA(*ys), LA(*yst),
+        ctypes.c_void_p(_lib.stream_ptr(x.device, stream)))
+    if rc != 0:
+        raise RuntimeError(f"fp8_e4m3_gemv_multi returned {rc}")
+    return res
 
 
 def fp8_e4m3_swiglu_gemv(

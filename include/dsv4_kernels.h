@@ -12,6 +12,7 @@
  *                                                 mxfp4_dequant_bf16 (extension)
  *   kernel/fp8-dense/libfp8_e4m3_gemv.so          fp8_e4m3_gemv_m1,
  *                                                 fp8_e4m3_gemv, fp8_e4m3_gemv_grouped,
+ *                                                 fp8_e4m3_gemv_multi,
  *                                                 fp8_e4m3_swiglu_gemv, fp8_e4m3_rmsnorm_gemv,
  *                                                 fp8_e4m3_dequant_bf16 (extensions)
  *   kernel/rmsnorm-fuse/librmsnorm_fuse.so        rmsnorm_fuse_fwd,
@@ -301,6 +302,24 @@ int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_
                           dsv4_bf16_t* y, int64_t y_row_stride, int64_t y_group_stride,
                           hipStream_t stream);
 
+/* EXTENSION (replaces consecutive fp8_e4m3_gemv_m1 calls on one activation,
+ * e.g. wq_a and wkv on the normalised row, reference
+ * kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:395-418): n_mats GEMVs
+ * that share x, K and T in one launch,
+ *   y_m[t, n] = bf16( sum_k W_m[n, k] x[t, k] ),  n < N[m], m < n_mats,
+ * with the bits fp8_e4m3_gemv writes for each matrix alone. The per-matrix
+ * arguments are host arrays of n_mats entries (pointers are device pointers):
+ * W_fp8[m] [N[m], K] (row stride weight_row_stride_bytes[m]), W_scale[m]
+ * [ceil(N[m]/128), K/128] (scale_row_stride_bytes[m]), y[m] [T, N[m]] (row
+ * stride y_row_stride[m] elements); x [T, K] with row stride x_row_stride.
+ * K in {1024, 2048, 4096, 8192} with 16-byte aligned x, weights and rows runs
+ * as one launch; other shapes run one launch per matrix. Returns as
+ * fp8_e4m3_gemv, plus -6 for n_mats outside [1, 8] or a null table. */
+int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, int K, int T, int n_mats,
+                        const uint8_t* const* W_fp8, const uint8_t* const* W_scale, const int* N,
+                        const int64_t* weight_row_stride_bytes, const int64_t* scale_row_stride_bytes,
+                        dsv4_bf16_t* const* y, const int64_t* y_row_stride, hipStream_t stream);
+
 /* EXTENSION (replaces the gate GEMV, the up GEMV and the SwiGLU launch of the
  * shared expert, reference kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:
  * 508-548 and runtime/dsv4_engine_mxfp4.py:399-410): one launch for
@@ -309,8 +328,8 @@ int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_
  * fp8_e4m3_gemv writes), c a clamp to [-limit, limit] (no clamp for
  * limit <= 0), c_up the same clamp if clamp_up != 0 (runtime/dsv4_engine_mxfp4.py:
  * 405-407 clamps both) else none (dsv4_engine_mxfp4_wire.cu:517-518 clamps the
- * gate only). W1, W3 share K, N and row strides. Needs K in {2048, 4096} and
- * 16-byte aligned x, W1, W3 and rows (-6 otherwise); T in [1, 16] (-5).
+ * gate only). W1, W3 share K, N and row strides. Needs K in {1024, 2048, 4096,
+ * 8192} and 16-byte aligned x, W1, W3 and rows (-6 otherwise); T in [1, 16] (-5).
  * Returns as fp8_e4m3_gemv otherwise. */
 int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W1_fp8,
                          const uint8_t* W1_scale, const uint8_t* W3_fp8, const uint8_t* W3_scale,

@@ -25,6 +25,7 @@ LIBS = {
         "mxfp4_moe_routed_dispatch", "mxfp4_moe_grouped_gemv_noalloc"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
+                                      "fp8_e4m3_gemv_multi",
                                       "fp8_e4m3_swiglu_gemv", "fp8_e4m3_rmsnorm_gemv", "fp8_e4m3_dequant_bf16"],
     "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],
 }
@@ -280,8 +281,22 @@ def test_fp8_validation_codes():
     sw.argtypes = [P, L, P, P, P, P, I, I, I, L, L, ctypes.c_float, I, P, L, P]
     assert sw(N, 4096, N, N, N, N, 4096, 2048, 0, 4096, 32, 10.0, 1, N, 2048, N) == -5
     assert sw(N, 4096, N, N, N, N, 4000, 2048, 1, 4096, 32, 10.0, 1, N, 2048, N) == -1
-    # K = 1024 is a valid GEMV shape that the fused kernel does not take
-    assert sw(N, 1024, N, N, N, N, 1024, 2048, 1, 1024, 8, 10.0, 1, N, 2048, N) == -6
+    # K = 512 is a valid GEMV shape that the fused kernel does not take
+    assert sw(N, 512, N, N, N, N, 512, 2048, 1, 512, 4, 10.0, 1, N, 2048, N) == -6
+    mu = lib.fp8_e4m3_gemv_multi
+    mu.restype = I
+    mu.argtypes = [P, L, I, I, I] + [P] * 7 + [P]
+    PP = ctypes.c_void_p * 2
+    ptrs = PP(None, None)
+    Ns = (ctypes.c_int * 2)(1024, 512)
+    strides = (ctypes.c_int64 * 2)(4096, 4096)
+    assert mu(N, 4096, 4096, 1, 0, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -6   # n_mats < 1
+    assert mu(N, 4096, 4096, 1, 9, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -6   # n_mats > 8
+    assert mu(N, 4096, 4096, 1, 2, None, ptrs, Ns, strides, strides, ptrs, strides, N) == -6   # null table
+    assert mu(N, 4096, 4000, 1, 2, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -1   # K % 128
+    assert mu(N, 4096, 4096, 0, 2, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -5   # T < 1
+    Ns[1] = 0
+    assert mu(N, 4096, 4096, 1, 2, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -4   # N < 1
     rn = lib.fp8_e4m3_rmsnorm_gemv
     rn.restype = I
     rn.argtypes = [P, P, P, ctypes.c_float, P, P, I, I, I, L, L, P, P, P, P]

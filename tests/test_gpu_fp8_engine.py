@@ -1,0 +1,68 @@
+"""GPU parity of the FP8 GEMVs at the reference engine's MLA shapes
+(kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:395-418, 404, 501): the
+tile kernels at K = 1024 (wq_b, 32768 x 1024) and K = 8192 (wo_b, 4096 x
+8192), several tokens with the weights read once, and the multi-matrix launch
+(wq_a and wkv on one activation) against the oracle and, bit for bit, against
+one launch per matrix. Bar: max rel err <= 1e-2, cosine >= 0.9999."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import mx
+from runtime import fp8_e4m3_gemv_binding as fp8b
+from runtime import synth
+from tests.gpu_util import announce, assert_close, dev_bf16, dev_u8, host_bits
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("N,K,T", [(32768, 1024, 1), (4096, 1024, 3), (130, 1024, 16),
+                                   (4096, 8192, 1), (4096, 8192, 2), (4096, 8192, 5), (300, 8192, 16),
+                                   (4096, 4096, 16), (1000, 2048, 11)])
+def test_fp8_tile_engine_shapes(device, N, K, T):
+    """K = 1024 and 8192 on the tile path (16 and 2 rows per workgroup), and
+    token counts above the per-group register budget (4 at K = 8192, 16
+    otherwise), which loop over token groups with the weights in registers."""
+    announce(f"fp8_e4m3_gemv tile N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(15000 + N + K, N, K)
+    x = synth.normal_bf16(15100 + T + K, (T, K))
+    xd = dev_bf16(x, device)
+    y = fp8b.fp8_e4m3_gemv(dev_u8(w, device), dev_u8(s, device), xd if T > 1 else xd[0])
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 N={N} K={K} T={T}")
+
+
+@pytest.mark.parametrize("shapes,K,T", [([1536, 576], 4096, 1), ([1024, 512], 4096, 1), ([1536, 576], 4096, 4),
+                                        ([130, 700, 64], 2048, 2), ([4096, 1024], 8192, 3),
+                                        ([2048, 300], 1024, 1)])
+def test_fp8_gemv_multi(device, shapes, K, T):
+    """Several matrices on one activation in one launch: each output has the
+    bits of fp8_e4m3_gemv on that matrix alone and matches the oracle."""
+    announce(f"fp8_e4m3_gemv_multi N={shapes} K={K} T={T}")
+    mats, dmats = [], []
+    for i, N in enumerate(shapes):
+        w, s = synth.fp8_weight(15200 + 10 * i + N, N, K)
+        mats.append((w, s))
+        dmats.append((dev_u8(w, device), dev_u8(s, device)))
+    x = synth.normal_bf16(15300 + T, (T, K))
+    xd = dev_bf16(x, device)
+    xin = xd if T > 1 else xd[0]
+    ys = fp8b.fp8_e4m3_gemv_multi(dmats, xin)
+    for (w, s), (tw, ts), y, N in zip(mats, dmats, ys, shapes):
+        got = host_bits(y).reshape(T, N)
+        single = host_bits(fp8b.fp8_e4m3_gemv(tw, ts, xin)).reshape(T, N)
+        assert np.array_equal(got, single), f"N={N}: multi launch differs from the single launch"
+        assert_close(got, mx.fp8_gemv(x, w, s), f"multi N={N} K={K} T={T}")
+
+
+@pytest.mark.parametrize("N,K,T", [(2048, 8192, 1), (512, 1024, 3)])
+def test_fp8_swiglu_gemv_engine_k(device, N, K, T):
+    announce(f"fp8_e4m3_swiglu_gemv N={N} K={K} T={T}")
+    w1, s1 = synth.fp8_weight(15400 + N, N, K)
+    w3, s3 = synth.fp8_weight(15500 + N, N, K)
+    x = mx.bf16_round(24 * mx.bf16_to_f32(synth.normal_bf16(15600 + T, (T, K))))
+    xd = dev_bf16(x, device)
+    act = fp8b.fp8_e4m3_swiglu_gemv(dev_u8(w1, device), dev_u8(s1, device), dev_u8(w3, device),
+                                    dev_u8(s3, device), xd if T > 1 else xd[0], 10.0, False)
+    assert_close(host_bits(act).reshape(T, N), mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, False),
+                 f"fp8 swiglu N={N} K={K} T={T}")

@@ -148,7 +148,7 @@ def test_fp8_gemv_tile_path_tokens_and_ragged_n(device, N, K, T):
 
 def test_fp8_gemv_long_rows_and_ragged_n(device):
     N, K, T = 200, 8192, 3
-    announce(f"fp8_e4m3_gemv N={N} K={K} T={T} (two K segments)")
+    announce(f"fp8_e4m3_gemv N={N} K={K} T={T} (K = 8192 on the tile path)")
     w, s = synth.fp8_weight(4001, N, K)
     x = synth.normal_bf16(4002, (T, K))
     y = fp8b.fp8_e4m3_gemv(dev_u8(w, device), dev_u8(s, device), dev_bf16(x, device))
@@ -161,7 +161,7 @@ def test_fp8_gemv_grouped(device, G, N, K, T):
     """G GEMVs in one launch (the wo_a shape G=8, N=1024, K=4096 first): against
     the oracle, and, for 128-row groups on the tile path, bit for bit against
     one fp8_e4m3_gemv call per group on that group's slice. N=576 and N=64
-    put group boundaries inside a scale tile; K=1024 takes the general kernel."""
+    put group boundaries inside a scale tile."""
     announce(f"fp8_e4m3_gemv_grouped G={G} N={N} K={K} T={T}")
     w, s = synth.fp8_weight(4300 + G + N, G * N, K)
     x = synth.normal_bf16(4400 + T, (T, G, K))
