@@ -4,28 +4,30 @@
 One step = one routed-MoE layer at decode (mxfp4_moe_layer): device gating of
 N(0,1) logits over 256 experts (top-8, sigmoid weights renormalised) with the
 routing tables, then stage A (W1/W3 + SiLU) and stage B (W2 + weighted combine)
-of the expert-indexed MXFP4 grouped GEMV. At T=1 the gating runs inside stage A
-(two launches); for T>1 it is a launch of its own. The kernels read the routed
-experts in place from HBM-resident per-layer tensors. The
-K timed steps are timed twice, each time over all K steps: issued from the
-host loop (two or three launches per step on one stream), and captured in a
-HIP graph and replayed. The faster of the two is the headline (`timing` names
-it) and both are reported: on this ROCm build a replayed graph leaves more
-time between dependent kernels than host-issued launches at T=1 (the layer
-measured 23.4-23.7 against 24.1-25.0 us), while a host loop that issues many
-launches per step (config 4) is bound by the host. Inputs are resident in HBM
-before the timed region. Steps
-cycle over --layers layers of 256 experts (4 x 3.42 GB by default) with fresh
-logits each step, so weights come from HBM, not the 256 MB MALL.
+of the expert-indexed MXFP4 grouped GEMV, reading the routed experts in place
+from HBM-resident per-layer tensors. At T=1 the gating runs inside stage A
+(two launches); for T>1 it is a launch of its own. The K timed steps are timed
+twice over all K steps: issued from the host loop, and captured in a HIP graph
+and replayed; the faster is the headline (`timing` names it). Inputs are
+resident in HBM before the timed region, and the steps cycle over --layers
+layers of 256 experts (4 x 3.42 GB) with fresh logits each step, so weights
+come from HBM, not the 256 MB MALL.
 
 Prints ONE JSON line. `value` is the layer's algorithmic HBM bytes per step
 (unique routed experts x 13,369,344 B + activations + routing) divided by the
-step time, in GB/s. `roofline` covers the dominant kernel (stage A), timed
-alone over back-to-back launches with HIP events. `cpu_baseline` times the
-CPU oracle (dequant + fp32 matmul, the reference's CPU path) on one step, and
-the same layer with the weights dequantised beforehand (matmul only).
+step time, in GB/s. `roofline` covers the dominant kernel of that step, the
+gated one-token stage A (moe_swiglu_t1_kernel with the gating folded in), timed
+alone over back-to-back launches with HIP events on the launch stream;
+`stage_b_roofline` the same for stage B. `configs` holds the other
+configurations measured in the same run (config 3 at T=4 and T=16, the
+reference's routed dispatch, config 4's 43-layer decode sweep and its 512-token
+prefill chunk), `kernels` the other drop-in kernels at BASELINE.json's shapes
+and the engine's FP8 shapes. `cpu_baseline` times the CPU oracle (dequant +
+fp32 matmul, the reference's CPU path) on one step.
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--layers L]
+                    [--no-configs] [--no-kernels] [--no-cpu-baseline]
+    python bench.py --counters     # a short fixed sequence for rocprofv3 counter passes
 """
 from __future__ import annotations
 
@@ -46,28 +48,26 @@ import numpy as np  # noqa: E402
 
 METRIC = "MoE-layer decode µs + MXFP4 grouped GEMV HBM GB/s (% of MI355X peak)"
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 E, K, H, O, TOPK = 256, 4096, 2048, 4096, 8
 EXPERT_BYTES = 3 * (H * K // 2 + H * K // 32)          # 13,369,344 B (W1 + W3 + W2, packed + scales)
 STAGE_A_EXPERT_BYTES = 2 * (H * K // 2 + H * K // 32)  # 8,912,896 B (W1 + W3)
 STAGE_B_EXPERT_BYTES = O * H // 2 + O * H // 32         # 4,456,448 B (W2)
-STAGE_A_KERNEL = {1: "moe_swiglu_t1_kernel"}            # stage A's kernel by T (default: the multi-token kernel)
-STAGE_A_KERNEL_MULTI = "moe_swiglu_tn_kernel"
+MALL_DEFEAT_BYTES = 512 << 20                           # rotate weight copies over >= 2x the 256 MB MALL
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def topk_ids(logits: np.ndarray) -> np.ndarray:
-    return np.argsort(-logits.astype(np.float64), axis=1, kind="stable")[:, :TOPK]
+def topk_ids(logits: np.ndarray, k: int = TOPK) -> np.ndarray:
+    return np.argsort(-logits.astype(np.float64), axis=1, kind="stable")[:, :k]
 
 
 def profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` (a kernel name and the token count it
-    was measured at, e.g. "moe_swiglu_t1_kernel@T1") as measured by rocprofv3
-    counter passes (FETCH_SIZE and WRITE_SIZE, each scaled by what it reads for
-    a plain copy of known size). The summaries live in profiles/*.md as lines
-    `TRAFFIC <kernel>@T<tokens> <bytes>`; returns (bytes, file) or (None, None)."""
+    """HBM bytes per launch of `kernel` ("name@T<tokens>") from the rocprofv3
+    counter summaries in profiles/*.md (lines `TRAFFIC <kernel>@T<tokens>
+    <bytes>`); returns (bytes, file) or (None, None)."""
     d = os.path.join(REPO, "profiles")
     if not os.path.isdir(d):
         return None, None
@@ -82,24 +82,270 @@ def profiled_traffic(kernel: str):
     return None, None
 
 
-MALL_DEFEAT_BYTES = 512 << 20   # rotate weight copies over >= 2x the 256 MB MALL
+def gbs(nbytes: float, us: float) -> float:
+    return nbytes / (us * 1e-6) / 1e9
 
 
-def dense_kernels(torch, dev, cpu: bool) -> dict:
-    """The other three drop-in kernels at their BASELINE.json shapes: dense
-    MXFP4 GEMV, FP8-E4M3 GEMV (configs[2], T in {1, 8}) and
-    fused RMSNorm + residual (configs[1], T in {1, 8, 64}). Each case replays a
-    HIP graph of launches that rotate over enough weight copies (>= 512 MB) for
-    the weights to come from HBM; µs per launch, algorithmic GB/s and the
-    fraction of 8 TB/s are reported, with the CPU oracle's time for one call
-    beside it (cpu=True)."""
+class Timer:
+    """HIP events on torch's current stream, which is the stream every
+    binding launches on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.e0 = torch.cuda.Event(enable_timing=True)
+        self.e1 = torch.cuda.Event(enable_timing=True)
+
+    def ms(self, fn) -> float:
+        self.torch.cuda.synchronize()
+        self.e0.record()
+        fn()
+        self.e1.record()
+        self.torch.cuda.synchronize()
+        return self.e0.elapsed_time(self.e1)
+
+    def graph_us_per_call(self, fn, n_calls: int, reps: int = 2) -> float:
+        """Capture fn() (n_calls launches) once, replay; µs per call."""
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        us = self.ms(lambda: [g.replay() for _ in range(reps)]) * 1e3 / (reps * n_calls)
+        del g
+        return us
+
+
+# ------------------------------------------------------------ config 3 ------
+
+def moe_layer_case(torch, dev, layers, T: int, steps: int, warmup: int, seed: int, stages: bool = True) -> dict:
+    """Config 3 at T tokens: the layer step (graph and host-issued, the faster
+    is reported) and, with `stages`, each launch alone over back-to-back
+    launches: the gating + stage A launch(es) (mxfp4_moe_gate_swiglu), stage A
+    on given tables (mxfp4_moe_swiglu) and stage B (mxfp4_moe_down)."""
+    from runtime import moe, synth
+    from runtime import mxfp4_grouped_gemv_binding as gb
+
+    L = len(layers)
+    tm = Timer(torch)
+    n = warmup + steps
+    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=max(16, T), check=False) for w in layers]
+    x = torch.from_numpy(synth.normal_bf16(seed, (T, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+    logits_h = synth.gating_logits(seed + 1, n * T, E).reshape(n, T, E)
+    logits = torch.from_numpy(logits_h).to(dev)
+    uniq = np.array([len(np.unique(topk_ids(logits_h[i]))) for i in range(n)])
+    step_bytes = uniq * EXPERT_BYTES + 2 * T * K * 2 + T * TOPK * 8 + T * E * 4
+
+    def step(i):
+        mods[i % L].forward(x, logits=logits[i])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    graph_us = tm.graph_us_per_call(lambda: [step(i) for i in range(warmup, n)], steps, reps=1)
+    host_us = tm.ms(lambda: [step(i) for i in range(warmup, n)]) * 1e3 / steps
+    us = min(graph_us, host_us)
+    timed_bytes = float(step_bytes[warmup:].mean())
+    out = {
+        "tokens": T,
+        "moe_layer_us": round(us, 3),
+        "moe_layer_us_graph": round(graph_us, 3),
+        "moe_layer_us_host_issued": round(host_us, 3),
+        "timing": "HIP graph replay" if graph_us <= host_us else "launches issued from the host loop",
+        "gbs": round(gbs(timed_bytes, us), 1),
+        "hbm_frac_of_peak": round(gbs(timed_bytes, us) / HBM_PEAK_GBS, 4),
+        "mean_unique_experts": round(float(uniq[warmup:].mean()), 3),
+        "algorithmic_bytes_per_step": int(round(timed_bytes)),
+    }
+    if not stages:
+        return out
+    # Each launch alone: R steps' worth of routing states, launched back to back.
+    R = min(32, n)
+    sts = []
+    for i in range(R):
+        st = gb.MoEStages(layers[i % L].W1, layers[i % L].W3, layers[i % L].W2, T, TOPK, dev)
+        st.gate_swiglu(x, logits[i])
+        sts.append(st)
+    yo = torch.empty(T, O, dtype=torch.bfloat16, device=dev)
+    for st in sts:
+        st.down(yo)
+    torch.cuda.synchronize()
+    a_gate_us = tm.graph_us_per_call(lambda: [st.gate_swiglu(x, logits[i]) for i, st in enumerate(sts)], R, reps=2)
+    a_us = tm.graph_us_per_call(lambda: [st.swiglu(x) for st in sts], R, reps=2)
+    b_us = tm.graph_us_per_call(lambda: [st.down(yo) for st in sts], R, reps=2)
+    a_bytes = float(np.mean(uniq[:R] * STAGE_A_EXPERT_BYTES + T * K * 2 + T * E * 4))
+    b_bytes = float(np.mean(uniq[:R] * STAGE_B_EXPERT_BYTES + T * O * 2))
+    out["stage_us"] = {"gate_swiglu_A": round(a_gate_us, 3), "swiglu_A_tables_given": round(a_us, 3),
+                       "down_B": round(b_us, 3)}
+    out["stage_gbs"] = {"gate_swiglu_A": round(gbs(a_bytes, a_gate_us), 1),
+                        "swiglu_A_tables_given": round(gbs(a_bytes, a_us), 1),
+                        "down_B": round(gbs(b_bytes, b_us), 1)}
+    out["_stage_bytes"] = (a_bytes, b_bytes)
+    del sts
+    return out
+
+
+def routed_dispatch_case(torch, dev, layers, steps: int, warmup: int) -> dict:
+    """The reference engine's routed dispatch on the device
+    (mxfp4_moe_routed_dispatch: router GEMV over a bf16 [256, 4096] gate,
+    sqrt-softplus top-6 x 1.5, expert-indexed grouped GEMV) at T=1, cycling
+    over the resident layers; replaces kernel/cpp-engine-mxfp4/routed.cu:373-503
+    (host sync, 36 pack copies, grouped GEMV)."""
+    from runtime import fill, moe, synth
+
+    L = len(layers)
+    k = 6
+    tm = Timer(torch)
+    gates = []
+    for l in range(L):
+        # bf16 gate rows of seeded random bits, masked to finite values below
+        # 2^-5 (sign bit cleared; timing does not depend on the values)
+        g = torch.empty(E, K, dtype=torch.bfloat16, device=dev)
+        fill.fill_uniform_u8(g.view(torch.uint8), 5000 + l, 0, 0, 255)
+        g.view(torch.int16).bitwise_and_(0x3CFF)
+        gates.append(g)
+    mods = [moe.RoutedMoELayer(w, topk=k, max_tokens=1, check=False, router_gate=gates[l])
+            for l, w in enumerate(layers)]
+    n = warmup + steps
+    xs = torch.from_numpy(synth.normal_bf16(3500, (n, 1, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+
+    def step(i):
+        mods[i % L].forward(xs[i])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    graph_us = tm.graph_us_per_call(lambda: [step(i) for i in range(warmup, n)], steps, reps=1)
+    host_us = tm.ms(lambda: [step(i) for i in range(warmup, n)]) * 1e3 / steps
+    us = min(graph_us, host_us)
+    nbytes = k * EXPERT_BYTES + E * K * 2 + 2 * K * 2 + k * 8
+    return {
+        "tokens": 1, "topk": k, "routed_scale": 1.5,
+        "us": round(us, 3), "us_graph": round(graph_us, 3), "us_host_issued": round(host_us, 3),
+        "algorithmic_bytes_per_step": int(nbytes),
+        "gbs": round(gbs(nbytes, us), 1), "hbm_frac_of_peak": round(gbs(nbytes, us) / HBM_PEAK_GBS, 4),
+        "launches": 3,
+        "kernels": "router GEMV (mxfp4_moe_router_logits' kernel), gated stage A with sqrt-softplus scoring, stage B",
+    }
+
+
+# ------------------------------------------------------------ config 4 ------
+
+def config4_case(torch, dev, steps: int, warmup: int, n_layers: int = 43) -> dict:
+    """a decode sweep over n_layers layers whose 256
+    MXFP4 experts are all resident in HBM (147 GB at 43 layers). Each layer
+    has a seeded Zipf(1.1) expert popularity; each step routes one token per
+    layer by Gumbel-top-8 (runtime.synth.zipf_routing). One step = the
+    n_layers routed layers (ids given: mxfp4_moe_grouped_gemv, two launches
+    per layer), the layer's input being the previous layer's output (a
+    chained decode). Then one 512-token prefill chunk per layer through the
+    MFMA grouped GEMM."""
+    from runtime import moe, synth
+    from runtime import mxfp4_grouped_gemv_binding as gb
+
+    tm = Timer(torch)
+    t0 = time.perf_counter()
+    log(f"configs[4]: allocating and filling {n_layers} layers x {E} experts "
+        f"({n_layers * E * EXPERT_BYTES / 1e9:.1f} GB)")
+    layers = [moe.make_moe_weights(40000 + 100 * l, E, K, H, O, dev) for l in range(n_layers)]
+    torch.cuda.synchronize()
+    fill_s = time.perf_counter() - t0
+    n = warmup + steps
+    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=1, check=False) for w in layers]
+    ids_h, ids_d, w_d = [], [], []
+    for l in range(n_layers):
+        ids, w = synth.zipf_routing(4000, n, E, TOPK, 1.1, layer=l)
+        ids_h.append(ids)
+        ids_d.append(torch.from_numpy(ids).to(dev))
+        w_d.append(torch.from_numpy(w).to(dev))
+    x0 = torch.from_numpy(synth.normal_bf16(4001, (1, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+
+    def step(i):
+        # layer l reads layer l-1's output in place (each layer owns its output buffer)
+        x = x0
+        for l in range(n_layers):
+            x = mods[l].forward(x, ids=ids_d[l][i:i + 1], weights=w_d[l][i:i + 1])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    graph_ms = tm.graph_us_per_call(lambda: [step(i) for i in range(warmup, n)], steps, reps=1) / 1e3
+    host_ms = tm.ms(lambda: [step(i) for i in range(warmup, n)]) / steps
+    ms = min(graph_ms, host_ms)
+    uniq = sum(len(np.unique(ids_h[l][i])) for l in range(n_layers) for i in range(warmup, n))
+    step_bytes = uniq / steps * EXPERT_BYTES + n_layers * (2 * K * 2 + TOPK * 8)
+    decode = {
+        "layers": n_layers, "tokens": 1, "steps": steps,
+        "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / n_layers, 3),
+        "us_per_layer_graph": round(graph_ms * 1e3 / n_layers, 3),
+        "us_per_layer_host_issued": round(host_ms * 1e3 / n_layers, 3),
+        "timing": "HIP graph replay" if graph_ms <= host_ms else "launches issued from the host loop",
+        "algorithmic_bytes_per_step": int(step_bytes),
+        "gbs": round(gbs(step_bytes, ms * 1e3), 1),
+        "hbm_frac_of_peak": round(gbs(step_bytes, ms * 1e3) / HBM_PEAK_GBS, 4),
+        "resident_gb": round(n_layers * E * EXPERT_BYTES / 1e9, 2),
+        "fill_seconds": round(fill_s, 1),
+        "note": "a chained decode: each layer reads the previous layer's output",
+    }
+    # One 512-token prefill chunk per layer (MFMA grouped GEMM), graph-replayed.
+    TP = 512
+    xp = torch.from_numpy(synth.normal_bf16(4002, (TP, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+    pre_ids, pre_w, pre_uniq = [], [], 0
+    for l in range(n_layers):
+        ids, w = synth.zipf_routing(4003, TP, E, TOPK, 1.1, layer=l)
+        pre_uniq += len(np.unique(ids))
+        pre_ids.append(torch.from_numpy(ids).to(dev))
+        pre_w.append(torch.from_numpy(w).to(dev))
+    ws = torch.empty(gb.prefill_workspace_bytes(TP, TOPK, E, H, O), dtype=torch.uint8, device=dev)
+    yout = torch.empty(TP, O, dtype=torch.bfloat16, device=dev)
+
+    def prefill_all():
+        for l in range(n_layers):
+            gb.mxfp4_moe_prefill(xp, layers[l].W1, layers[l].W3, layers[l].W2, pre_ids[l], pre_w[l],
+                                 out=yout, workspace=ws)
+
+    prefill_all()
+    torch.cuda.synchronize()
+    pre_us = tm.graph_us_per_call(prefill_all, n_layers, reps=1)
+    pre_bytes = pre_uniq / n_layers * EXPERT_BYTES + TP * K * 2 + TP * O * 2
+    pre_flop = 2.0 * TP * TOPK * (2 * K * H + H * O)
+    prefill = {
+        "tokens": TP, "layers": n_layers, "us_per_layer": round(pre_us, 2),
+        "mean_unique_experts": round(pre_uniq / n_layers, 2),
+        "algorithmic_bytes_per_layer": int(pre_bytes),
+        "gbs": round(gbs(pre_bytes, pre_us), 1),
+        "hbm_frac_of_peak": round(gbs(pre_bytes, pre_us) / HBM_PEAK_GBS, 4),
+        "tflops": round(pre_flop / (pre_us * 1e-6) / 1e12, 1),
+        "mfma_frac_of_bf16_peak": round(pre_flop / (pre_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "kernel": "v_mfma_f32_16x16x32_bf16 on exactly dequantised MXFP4 weights (4 launches per layer)",
+    }
+    del layers, mods, ws
+    torch.cuda.empty_cache()
+    return {"decode": decode, "prefill": prefill}
+
+
+# ------------------------------------------------------- dense kernels ------
+
+def dense_kernels(torch, dev, cpu: bool, counters: bool = False) -> dict:
+    """The other drop-in kernels at BASELINE.json's shapes (dense MXFP4
+    configs[0], FP8 configs[2] at T in {1, 8}, RMSNorm + residual configs[1] at
+    T in {1, 8, 64}), the FP8 launches at the reference engine's MLA shapes
+    (dsv4_engine_mxfp4_wire.cu:395-501), the fused FP8 call sites and the
+    router GEMV. Each case replays a HIP graph of at most 2,048 launches that
+    rotate over weight copies totalling >= 512 MB (so weights come from HBM),
+    µs per launch (launch floor included), algorithmic GB/s and the fraction
+    of 8 TB/s, with the CPU oracle's time for one call beside it (cpu=True).
+    counters=True runs 32 eager launches per case instead (rocprofv3 counter
+    passes)."""
     from oracle import mx  # CPU baseline only
+    from runtime import fill
     from runtime import fp8_e4m3_gemv_binding as fp8b
     from runtime import mxfp4_gemv_binding as mxb
+    from runtime import mxfp4_grouped_gemv_binding as gb
     from runtime import rmsnorm_fuse_binding as rb
     from runtime import synth
 
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    tm = Timer(torch)
 
     def u8(a):
         return torch.from_numpy(np.ascontiguousarray(a, np.uint8)).to(dev)
@@ -110,38 +356,38 @@ def dense_kernels(torch, dev, cpu: bool) -> dict:
     def rep(t, n):
         return t.unsqueeze(0).repeat(n, *([1] * t.dim()))
 
+    def n_copies(nbytes_per_copy):
+        return max(2, -(-MALL_DEFEAT_BYTES // nbytes_per_copy))
+
     def copies(t, nbytes_per_copy):
-        n = max(2, -(-MALL_DEFEAT_BYTES // nbytes_per_copy))
+        n = n_copies(nbytes_per_copy)
         return rep(t, n), n
 
-    def time_launches(fn, n_copies, reps=4):
+    def time_launches(fn, n_cop):
+        if counters:
+            for i in range(32):
+                fn(i % n_cop)
+            torch.cuda.synchronize()
+            return float("nan")
         fn(0)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        n = max(n_copies, 64)
-        with torch.cuda.graph(g):
-            for i in range(n):
-                fn(i % n_copies)
-        g.replay()
-        torch.cuda.synchronize()
-        ev0.record()
-        for _ in range(reps):
-            g.replay()
-        ev1.record()
-        torch.cuda.synchronize()
-        return ev0.elapsed_time(ev1) * 1e3 / (reps * n)
+        n = min(max(n_cop, 64), 2048)
+        return tm.graph_us_per_call(lambda: [fn(i % n_cop) for i in range(n)], n, reps=4)
 
     def cpu_us(fn):
-        if not cpu:
+        if not cpu or counters:
             return None
         t0 = time.perf_counter()
         fn()
         return round((time.perf_counter() - t0) * 1e6, 1)
 
-    def entry(us, nbytes, cpu_time):
-        gbs = nbytes / (us * 1e-6) / 1e9
-        return {"us": round(us, 3), "algorithmic_bytes": int(nbytes), "gbs": round(gbs, 1),
-                "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "cpu_oracle_us": cpu_time}
+    def entry(us, nbytes, cpu_time, extra=None):
+        g = gbs(nbytes, us)
+        e = {"us": round(us, 3), "algorithmic_bytes": int(nbytes), "gbs": round(g, 1),
+             "frac_of_peak": round(g / HBM_PEAK_GBS, 4), "cpu_oracle_us": cpu_time}
+        if extra:
+            e.update(extra)
+        return e
 
     out = {}
     # MXFP4 dense 2048 x 4096
@@ -157,79 +403,104 @@ def dense_kernels(torch, dev, cpu: bool) -> dict:
                                             cpu_us(lambda: mx.mxfp4_gemv(x0, p[0], s[0])))
     del P, S
     # FP8 GEMVs, T in {1, 8}
-    for (N, K) in ((1536, 4096), (576, 4096), (4096, 4096), (4096, 2048)):
-        w, ws = synth.fp8_weight(1002 + N + K, N, K)
-        wbytes = N * K + ws.size
+    for (N, Kf) in ((1536, 4096), (576, 4096), (4096, 4096), (4096, 2048)):
+        w, ws = synth.fp8_weight(1002 + N + Kf, N, Kf)
+        wbytes = N * Kf + ws.size
         W, nW = copies(u8(w), wbytes)
         WS = rep(u8(ws), nW)
         for T in (1, 8):
-            xh = synth.normal_bf16(2002 + T, (T, K))
-            xd = bf(xh) if T > 1 else bf(xh[0])
+            xh = synth.normal_bf16(2002 + T, (T, Kf))
+            xdt = bf(xh) if T > 1 else bf(xh[0])
             y = torch.empty((T, N) if T > 1 else (N,), dtype=torch.bfloat16, device=dev)
-            us = time_launches(lambda i: fp8b.fp8_e4m3_gemv(W[i], WS[i], xd, out=y), nW)
-            out[f"fp8_e4m3_gemv {N}x{K} T={T}"] = entry(us, wbytes + T * (2 * K + 2 * N),
-                                                         cpu_us(lambda: mx.fp8_gemv(xh, w, ws)))
+            us = time_launches(lambda i: fp8b.fp8_e4m3_gemv(W[i], WS[i], xdt, out=y), nW)
+            out[f"fp8_e4m3_gemv {N}x{Kf} T={T}"] = entry(us, wbytes + T * (2 * Kf + 2 * N),
+                                                          cpu_us(lambda: mx.fp8_gemv(xh, w, ws)))
         del W, WS
-    # Extensions on the same FP8 path: the grouped output projection wo_a
-    # (8 groups of 1024 x 4096 in one launch, against 8 single launches) and
-    # the shared expert's gate + up + SwiGLU (2048 x 4096 twice in one launch,
-    # against the two single GEMVs alone).
-    G, N, K = 8, 1024, 4096
-    w, ws = synth.fp8_weight(1100, G * N, K)
-    wbytes = G * N * K + ws.size
+
+    # The engine's MLA shapes (kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu):
+    # wq_a 1024x4096 and wkv 512x4096 on one activation (one multi launch
+    # against two single launches), wq_b 32768x1024, wo_b 4096x8192. Weights
+    # are device-filled E4M3 codes (positive, finite) with E8M0 tile scales.
+    def fp8_dev(seed, N, Kf):
+        w = torch.empty(N, Kf, dtype=torch.uint8, device=dev)
+        fill.fill_uniform_u8(w, seed, 0, 0, 0x7E)
+        s = torch.empty((N + 127) // 128, Kf // 128, dtype=torch.uint8, device=dev)
+        fill.fill_uniform_u8(s, seed + 1, 0, 119, 125)
+        return w, s
+
+    xe = bf(synth.normal_bf16(2100, (8, 8192)))
+    for name, N, Kf in (("wq_b", 32768, 1024), ("wo_b", 4096, 8192)):
+        w, s = fp8_dev(2200 + N, N, Kf)
+        wbytes = N * Kf + s.numel()
+        n = n_copies(wbytes)
+        W, WS = rep(w, n), rep(s, n)
+        for T in (1, 8):
+            xdt = xe[:T, :Kf].contiguous() if T > 1 else xe[0, :Kf].contiguous()
+            y = torch.empty((T, N) if T > 1 else (N,), dtype=torch.bfloat16, device=dev)
+            us = time_launches(lambda i: fp8b.fp8_e4m3_gemv(W[i], WS[i], xdt, out=y), n)
+            out[f"fp8_e4m3_gemv {name} {N}x{Kf} T={T}"] = entry(us, wbytes + T * (2 * Kf + 2 * N), None)
+        del W, WS
+    wa, sa = fp8_dev(2300, 1024, 4096)
+    wk, sk = fp8_dev(2301, 512, 4096)
+    wbytes = wa.numel() + sa.numel() + wk.numel() + sk.numel()
+    n = n_copies(wbytes)
+    WA, SA, WK, SK = rep(wa, n), rep(sa, n), rep(wk, n), rep(sk, n)
+    xa = xe[0, :4096].contiguous()
+    ya = torch.empty(1024, dtype=torch.bfloat16, device=dev)
+    yk = torch.empty(512, dtype=torch.bfloat16, device=dev)
+    us = time_launches(lambda i: fp8b.fp8_e4m3_gemv_multi([(WA[i], SA[i]), (WK[i], SK[i])], xa, outs=[ya, yk]), n)
+    out["fp8_e4m3_gemv_multi wq_a 1024x4096 + wkv 512x4096 T=1"] = entry(us, wbytes + 2 * 4096 + 2 * 1536, None)
+
+    def two_single(i):
+        fp8b.fp8_e4m3_gemv(WA[i], SA[i], xa, out=ya)
+        fp8b.fp8_e4m3_gemv(WK[i], SK[i], xa, out=yk)
+
+    us = time_launches(two_single, n)
+    out["fp8_e4m3_gemv_m1 x 2 wq_a + wkv (reference call pattern)"] = entry(us, wbytes + 2 * 4096 + 2 * 1536, None)
+    del WA, SA, WK, SK
+
+    # Extensions on the FP8 path: the grouped output projection wo_a (8 groups
+    # of 1024 x 4096 in one launch) and the shared expert's gate + up + SwiGLU.
+    G, N, Kf = 8, 1024, 4096
+    w, ws = synth.fp8_weight(1100, G * N, Kf)
+    wbytes = G * N * Kf + ws.size
     W, nW = copies(u8(w), wbytes)
     WS = rep(u8(ws), nW)
-    xh = synth.normal_bf16(1101, (G, K))
-    xd = bf(xh)
+    xh = synth.normal_bf16(1101, (G, Kf))
+    xdt = bf(xh)
     y = torch.empty(G, N, dtype=torch.bfloat16, device=dev)
-    us = time_launches(lambda i: fp8b.fp8_e4m3_gemv_grouped(W[i], WS[i], xd, G, out=y), nW)
+    us = time_launches(lambda i: fp8b.fp8_e4m3_gemv_grouped(W[i], WS[i], xdt, G, out=y), nW)
     out["fp8_e4m3_gemv_grouped wo_a 8x1024x4096 T=1"] = entry(
-        us, wbytes + 2 * G * K + 2 * G * N, cpu_us(lambda: mx.fp8_gemv_grouped(xh, w, ws, G)))
-
-    def per_group(i):
-        for g in range(G):
-            fp8b.fp8_e4m3_gemv(W[i][g * N:(g + 1) * N], WS[i][g * N // 128:(g + 1) * N // 128], xd[g], out=y[g])
-
-    us = time_launches(per_group, nW)
-    out["fp8_e4m3_gemv_m1 x 8 wo_a (reference call pattern)"] = entry(us, wbytes + 2 * G * K + 2 * G * N, None)
+        us, wbytes + 2 * G * Kf + 2 * G * N, cpu_us(lambda: mx.fp8_gemv_grouped(xh, w, ws, G)))
     del W, WS
-    N, K = 2048, 4096
-    w1, s1 = synth.fp8_weight(1102, N, K)
-    w3, s3 = synth.fp8_weight(1103, N, K)
-    wbytes = N * K + s1.size
+    N, Kf = 2048, 4096
+    w1, s1 = synth.fp8_weight(1102, N, Kf)
+    w3, s3 = synth.fp8_weight(1103, N, Kf)
+    wbytes = N * Kf + s1.size
     W1, nW = copies(u8(w1), 2 * wbytes)
     S1 = rep(u8(s1), nW)
     W3, S3 = rep(u8(w3), nW), rep(u8(s3), nW)
-    xh = synth.normal_bf16(1104, (K,))
-    xd = bf(xh)
+    xh = synth.normal_bf16(1104, (Kf,))
+    xdt = bf(xh)
     y = torch.empty(N, dtype=torch.bfloat16, device=dev)
-    y3 = torch.empty(N, dtype=torch.bfloat16, device=dev)
-    us = time_launches(lambda i: fp8b.fp8_e4m3_swiglu_gemv(W1[i], S1[i], W3[i], S3[i], xd, 10.0, True, out=y), nW)
+    us = time_launches(lambda i: fp8b.fp8_e4m3_swiglu_gemv(W1[i], S1[i], W3[i], S3[i], xdt, 10.0, True, out=y), nW)
     out["fp8_e4m3_swiglu_gemv shared expert 2x2048x4096 T=1"] = entry(
-        us, 2 * wbytes + 2 * K + 2 * N, cpu_us(lambda: mx.fp8_swiglu(xh, w1, s1, w3, s3, 10.0, True)))
-
-    def two_gemvs(i):
-        fp8b.fp8_e4m3_gemv(W1[i], S1[i], xd, out=y)
-        fp8b.fp8_e4m3_gemv(W3[i], S3[i], xd, out=y3)
-
-    us = time_launches(two_gemvs, nW)
-    out["fp8_e4m3_gemv_m1 x 2 gate+up alone (reference call pattern, before its SwiGLU launch)"] = entry(
-        us, 2 * wbytes + 2 * K + 4 * N, None)
+        us, 2 * wbytes + 2 * Kf + 2 * N, cpu_us(lambda: mx.fp8_swiglu(xh, w1, s1, w3, s3, 10.0, True)))
     del W1, S1, W3, S3
-    # RMSNorm + residual folded into the wq_a GEMV (1536 x 4096), against the
-    # two launches (RMSNorm, then the GEMV on its output).
-    N, K = 1536, 4096
-    w, ws = synth.fp8_weight(1105, N, K)
-    wbytes = N * K + ws.size
+    # RMSNorm + residual folded into the wq_a GEMV (1536 x 4096).
+    N, Kf = 1536, 4096
+    w, ws = synth.fp8_weight(1105, N, Kf)
+    wbytes = N * Kf + ws.size
     W, nW = copies(u8(w), wbytes)
     WS = rep(u8(ws), nW)
-    hh, rh, gh = synth.normal_bf16(1106, (K,)), synth.normal_bf16(1107, (K,), 0.0, 0.5), synth.normal_bf16(1108, (K,), 1.0, 0.1)
+    hh, rh = synth.normal_bf16(1106, (Kf,)), synth.normal_bf16(1107, (Kf,), 0.0, 0.5)
+    gh = synth.normal_bf16(1108, (Kf,), 1.0, 0.1)
     hd, rd, gd = bf(hh), bf(rh), bf(gh)
-    xn = torch.empty(K, dtype=torch.bfloat16, device=dev)
-    nr = torch.empty(K, dtype=torch.bfloat16, device=dev)
+    xn = torch.empty(Kf, dtype=torch.bfloat16, device=dev)
+    nr = torch.empty(Kf, dtype=torch.bfloat16, device=dev)
     y = torch.empty(N, dtype=torch.bfloat16, device=dev)
     us = time_launches(lambda i: fp8b.fp8_e4m3_rmsnorm_gemv(W[i], WS[i], hd, gd, rd), nW)
-    nbytes = wbytes + 3 * 2 * K + 2 * K + 2 * 2 * K + 2 * N
+    nbytes = wbytes + 3 * 2 * Kf + 2 * Kf + 2 * 2 * Kf + 2 * N
     out["fp8_e4m3_rmsnorm_gemv residual+norm+wq_a 1536x4096 T=1"] = entry(us, nbytes, None)
 
     def two_launches(i):
@@ -239,148 +510,42 @@ def dense_kernels(torch, dev, cpu: bool) -> dict:
     us = time_launches(two_launches, nW)
     out["rmsnorm_fuse_residual_add + fp8_e4m3_gemv_m1 (two launches)"] = entry(us, nbytes, None)
     del W, WS
+    # Router gate GEMV of the routed dispatch: bf16 [256, 4096] x one token.
+    wg = torch.empty(E, K, dtype=torch.bfloat16, device=dev)
+    fill.fill_uniform_u8(wg.view(torch.uint8), 2400, 0, 0, 255)
+    wg.view(torch.int16).bitwise_and_(0x3CFF)
+    nbytes = E * K * 2
+    n = n_copies(nbytes)
+    WG = rep(wg, n)
+    xr = xe[0, :K].contiguous()
+    lo = torch.empty(1, E, dtype=torch.float32, device=dev)
+    us = time_launches(lambda i: gb.router_logits(xr, WG[i], out=lo), n)
+    out["router_logits bf16 256x4096 T=1"] = entry(us, nbytes + 2 * K + 4 * E, None)
+    del WG
     # RMSNorm + residual, H = 4096
-    H = 4096
-    g = synth.normal_bf16(1203, (H,), 1.0, 0.1)
-    gd = bf(g)
+    Hn = 4096
+    g = synth.normal_bf16(1203, (Hn,), 1.0, 0.1)
+    gdn = bf(g)
     for T in (1, 8, 64):
-        h = synth.normal_bf16(1201 + T, (T, H))
-        r = synth.normal_bf16(1301 + T, (T, H), 0.0, 0.5)
-        nb = 4 * T * H * 2
-        Hc, nH = copies(bf(h), nb)
-        Rc = rep(bf(r), nH)
-        yo = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-        ro = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-        us = time_launches(lambda i: rb.rmsnorm_fuse_residual_add(Hc[i], Rc[i], gd, out_norm=yo,
-                                                                  out_new_residual=ro), nH)
-        out[f"rmsnorm_fuse_residual_add T={T}x{H}"] = entry(us, nb + 2 * H,
-                                                            cpu_us(lambda: mx.rmsnorm_residual(h, r, g)))
+        h = synth.normal_bf16(1201 + T, (T, Hn))
+        r = synth.normal_bf16(1301 + T, (T, Hn), 0.0, 0.5)
+        nb = 4 * T * Hn * 2
+        # at most 2,048 activation copies per case (64 MB at T = 1): the
+        # activations are small enough that the launch floor, not HBM, bounds
+        # these launches
+        ncop = min(n_copies(nb), 2048)
+        Hc, Rc = rep(bf(h), ncop), rep(bf(r), ncop)
+        yo = torch.empty(T, Hn, dtype=torch.bfloat16, device=dev)
+        ro = torch.empty(T, Hn, dtype=torch.bfloat16, device=dev)
+        us = time_launches(lambda i: rb.rmsnorm_fuse_residual_add(Hc[i], Rc[i], gdn, out_norm=yo,
+                                                                  out_new_residual=ro), ncop)
+        out[f"rmsnorm_fuse_residual_add T={T}x{Hn}"] = entry(us, nb + 2 * Hn,
+                                                             cpu_us(lambda: mx.rmsnorm_residual(h, r, g)))
         del Hc, Rc
     return out
 
 
-def config4(args, torch, dev) -> dict:
-    """a decode sweep over a 43-layer MoE with every
-    layer's 256 MXFP4 experts resident in HBM (147 GB). Each layer has a seeded
-    expert popularity permutation with Zipf(s=1.1) ranks; each step routes one
-    token per layer by Gumbel-top-8 on log p (runtime.synth.zipf_routing) with
-    sigmoid(N(0,1)) weights renormalised. One step = the 43 routed MoE layers
-    (expert-indexed grouped GEMV, caller-given ids); the --steps steps are
-    captured in one HIP graph and replayed, and separately issued from the
-    host loop; the faster is the headline."""
-    from runtime import moe, synth
-
-    L4 = args.layers if args.layers != 4 else 43
-    S = args.steps
-    log(f"configs[4]: allocating {L4} layers x {E} experts ({L4 * E * EXPERT_BYTES / 1e9:.1f} GB)")
-    layers = [moe.make_moe_weights(40000 + 100 * l, E, K, H, O, dev) for l in range(L4)]
-    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=1, check=False) for w in layers]
-    ids_h, w_h, ids_d, w_d = [], [], [], []
-    for l in range(L4):
-        ids, w = synth.zipf_routing(4000, S + args.warmup, E, TOPK, 1.1, layer=l)
-        ids_h.append(ids)
-        ids_d.append(torch.from_numpy(ids).to(dev))
-        w_d.append(torch.from_numpy(w).to(dev))
-    x = torch.from_numpy(synth.normal_bf16(4001, (1, K)).view(np.int16)).view(torch.bfloat16).to(dev)
-    torch.cuda.synchronize()
-
-    def step(i):
-        for l in range(L4):
-            mods[l].forward(x, ids=ids_d[l][i:i + 1], weights=w_d[l][i:i + 1])
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    log(f"configs[4]: capturing {S} steps x {L4} layers in a HIP graph")
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(args.warmup, args.warmup + S):
-            step(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms_graph = ev0.elapsed_time(ev1) / S
-    del graph
-    log(f"configs[4]: timing {S} steps issued from the host")
-    torch.cuda.synchronize()
-    ev0.record()
-    for i in range(args.warmup, args.warmup + S):
-        step(i)
-    ev1.record()
-    torch.cuda.synchronize()
-    ms_host = ev0.elapsed_time(ev1) / S
-    ms = min(ms_graph, ms_host)
-    uniq = sum(len(np.unique(ids_h[l][i])) for l in range(L4) for i in range(args.warmup, args.warmup + S))
-    step_bytes = uniq / S * EXPERT_BYTES + L4 * (2 * K * 2 + TOPK * 8)
-    gbs = step_bytes / (ms * 1e-3) / 1e9
-
-    # One 512-token prefill chunk per layer through the MFMA grouped GEMM.
-    from runtime import mxfp4_grouped_gemv_binding as gb
-    TP = 512
-    log(f"configs[4]: prefill chunk of {TP} tokens per layer (MFMA grouped GEMM)")
-    xp = torch.from_numpy(synth.normal_bf16(4002, (TP, K)).view(np.int16)).view(torch.bfloat16).to(dev)
-    pre_ids, pre_w, pre_uniq = [], [], 0
-    for l in range(L4):
-        ids, w = synth.zipf_routing(4003, TP, E, TOPK, 1.1, layer=l)
-        pre_uniq += len(np.unique(ids))
-        pre_ids.append(torch.from_numpy(ids).to(dev))
-        pre_w.append(torch.from_numpy(w).to(dev))
-    ws = torch.empty(gb.prefill_workspace_bytes(TP, TOPK, E, H, O), dtype=torch.uint8, device=dev)
-    yout = torch.empty(TP, O, dtype=torch.bfloat16, device=dev)
-
-    def prefill_all():
-        for l in range(L4):
-            gb.mxfp4_moe_prefill(xp, layers[l].W1, layers[l].W3, layers[l].W2, pre_ids[l], pre_w[l],
-                                 out=yout, workspace=ws)
-
-    prefill_all()
-    torch.cuda.synchronize()
-    gp = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gp):
-        prefill_all()
-    gp.replay()
-    torch.cuda.synchronize()
-    ev0.record()
-    gp.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    pre_us = ev0.elapsed_time(ev1) * 1e3 / L4
-    pre_bytes = pre_uniq / L4 * EXPERT_BYTES + TP * K * 2 + TP * O * 2
-    pre_flop = 2.0 * TP * TOPK * (2 * K * H + H * O)
-    prefill = {
-        "tokens": TP, "us_per_layer": round(pre_us, 2),
-        "mean_unique_experts": round(pre_uniq / L4, 2),
-        "algorithmic_bytes_per_layer": int(pre_bytes),
-        "gbs": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1),
-        "hbm_frac_of_peak": round(pre_bytes / (pre_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "tflops": round(pre_flop / (pre_us * 1e-6) / 1e12, 1),
-        "mfma_frac_of_bf16_peak": round(pre_flop / (pre_us * 1e-6) / 2.5e15, 4),
-        "kernel": "v_mfma_f32_16x16x32_bf16 on exactly dequantised MXFP4 weights",
-    }
-    return {
-        "metric": "43-layer MoE decode step µs + MXFP4 grouped GEMV HBM GB/s (% of MI355X peak)",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": S, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "mxfp4-e2m1/e8m0 weights, bf16 activations, fp32 accumulate",
-        "data": "synthetic (seeded SplitMix64 weights filled on device; Zipf(1.1) Gumbel-top-8 routing)",
-        "config": {"workload": f"configs[4]: {L4}-layer MoE decode, T=1 per layer, top-{TOPK} of {E} "
-                               f"MXFP4 experts per layer, all {L4 * E} experts resident "
-                               f"({L4 * E * EXPERT_BYTES / 1e9:.1f} GB)",
-                   "layers": L4, "tokens": 1, "experts": E, "topk": TOPK,
-                   "algorithmic_bytes_per_step": int(step_bytes)},
-        "timing": ("HIP graph replay" if ms_graph <= ms_host else "launches issued from the host loop")
-                  + " (the faster of the two; HIP events on the launch stream)",
-        "us_per_layer": round(ms * 1e3 / L4, 3),
-        "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
-        "us_per_layer_graph": round(ms_graph * 1e3 / L4, 3),
-        "us_per_layer_host_issued": round(ms_host * 1e3 / L4, 3),
-        "prefill": prefill,
-    }
-
+# ----------------------------------------------------------- CPU baseline ---
 
 def cpu_model() -> str:
     try:
@@ -393,213 +558,184 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def cpu_baseline(torch, layer, x, logits_h, T: int, step_bytes: float) -> dict:
+    """The CPU oracle (the reference's CPU path: unpack + E8M0 -> bf16 dequant,
+    fp32 matmul, bf16 casts) on one step of the headline workload, on the
+    host's cores, and the same layer on weights dequantised beforehand."""
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle import mx
+
+    cache = {}
+
+    def expert(e):
+        if e not in cache:
+            cache[e] = tuple((m["packed"][e].cpu().numpy(), m["scale"][e].cpu().numpy())
+                             for m in (layer.W1, layer.W3, layer.W2))
+        return cache[e]
+
+    ids_t, w_t = mx.route_sigmoid_topk(logits_h, TOPK)
+    xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    for e in np.unique(ids_t):
+        expert(int(e))
+    threads = min(os.cpu_count() or 1, 16)
+    with threadpool_limits(limits=threads):
+        blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+        log(f"cpu baseline: oracle moe layer, {threads} BLAS threads")
+        t0 = time.perf_counter()
+        n_calls = 0
+        while True:
+            mx.moe_layer(xh, expert, ids_t, w_t, O)
+            n_calls += 1
+            if time.perf_counter() - t0 > 10.0 or n_calls >= 3:
+                break
+        cpu_s = (time.perf_counter() - t0) / n_calls
+        dq = {int(e): mx.dequant_expert_f32(expert(int(e))) for e in np.unique(ids_t)}
+        t0 = time.perf_counter()
+        n_mm = 0
+        while True:
+            mx.moe_layer_dequantised(xh, dq.__getitem__, ids_t, w_t, O)
+            n_mm += 1
+            if time.perf_counter() - t0 > 5.0 or n_mm >= 20:
+                break
+        mm_s = (time.perf_counter() - t0) / n_mm
+    return {
+        "value": round(step_bytes / cpu_s / 1e9, 4),
+        "unit": "GB/s",
+        "us_per_layer": round(cpu_s * 1e6, 1),
+        "matmul_only_us_per_layer": round(mm_s * 1e6, 1),
+        "cores": int(blas[0]) if blas else threads,
+        "kind": "port",
+        "sample": (f"{n_calls} call(s) of the numpy oracle moe_layer (unpack + E8M0 scale -> bf16 dequant, "
+                   f"fp32 matmul, bf16 casts) on step 0: T={T}, {len(np.unique(ids_t))} routed experts of "
+                   f"layer 0; host {cpu_model()}, nproc {os.cpu_count()}; matmul_only_us_per_layer: {n_mm} "
+                   f"call(s) of the same layer on weights dequantised to fp32 beforehand"),
+    }
+
+
+# -------------------------------------------------------------- counters ----
+
+def counters_run(torch, dev) -> int:
+    """A short fixed sequence for rocprofv3 --pmc passes (no HIP graphs, a
+    bounded number of dispatches): 24 one-token layers (gated stage A + stage
+    B) on 4 resident layers, 8 T=4 and 8 T=16 layers, then 32 launches of each
+    dense case. Kernel names identify the cases in the counter output."""
+    from runtime import moe, synth
+
+    layers = [moe.make_moe_weights(20000 + 100 * l, E, K, H, O, dev) for l in range(4)]
+    for T, n in ((1, 24), (4, 8), (16, 8)):
+        mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=16, check=False) for w in layers]
+        x = torch.from_numpy(synth.normal_bf16(3001, (T, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+        lg = torch.from_numpy(synth.gating_logits(3002, n * T, E).reshape(n, T, E)).to(dev)
+        for i in range(n):
+            mods[i % 4].forward(x, logits=lg[i])
+        torch.cuda.synchronize()
+        log(f"counters: {n} layers at T={T}")
+    del layers
+    torch.cuda.empty_cache()
+    dense_kernels(torch, dev, cpu=False, counters=True)
+    torch.cuda.synchronize()
+    log("counters: dense cases done")
+    return 0
+
+
+# ------------------------------------------------------------------ main ----
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--tokens", type=int, default=1, help="decode tokens per step (config 3: 1, 4, 16)")
+    ap.add_argument("--tokens", type=int, default=1, help="decode tokens per step of the headline (1, 4, 16)")
     ap.add_argument("--layers", type=int, default=4, help="resident layers cycled over (MALL defeat)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", type=int, default=3, choices=(3, 4),
-                    help="3: one routed MoE layer (the headline metric); 4: 43-layer decode sweep")
-    ap.add_argument("--no-kernels", action="store_true",
-                    help="skip the dense MXFP4 / FP8 / RMSNorm per-kernel lines")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the dense / FP8 / RMSNorm per-kernel lines")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations (config 3 at T=4/16, dispatch, config 4)")
+    ap.add_argument("--c4-layers", type=int, default=43, help="layers of the config-4 sweep")
+    ap.add_argument("--counters", action="store_true", help="short fixed sequence for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(the routed MoE would shard by experts, or by the ff dimension with one all-reduce "
-              "of the layer output per step)",
-              file=sys.stderr)
+              "of the layer output per step)", file=sys.stderr)
         return 2
 
     import torch
 
-    from runtime import moe, synth
-    from runtime import mxfp4_grouped_gemv_binding as gb
+    from runtime import moe
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    if args.config == 4:
-        print(json.dumps(config4(args, torch, dev)), flush=True)
-        return 0
+    if args.counters:
+        return counters_run(torch, dev)
+    t_start = time.perf_counter()
     T, L = args.tokens, args.layers
-    n_steps = args.warmup + args.steps
 
     log(f"allocating {L} layers x {E} experts ({L * E * EXPERT_BYTES / 1e9:.2f} GB)")
     layers = [moe.make_moe_weights(20000 + 100 * l, E, K, H, O, dev) for l in range(L)]
-    mods = [moe.RoutedMoELayer(w, topk=TOPK, max_tokens=max(16, T), check=False) for w in layers]
-    x = torch.from_numpy(synth.normal_bf16(3001, (T, K)).view(np.int16)).view(torch.bfloat16).to(dev)
-    logits_h = synth.gating_logits(3002, n_steps * T, E).reshape(n_steps, T, E)
-    logits = torch.from_numpy(logits_h).to(dev)
     torch.cuda.synchronize()
+    log(f"headline: config 3, T={T}, {args.steps} steps")
+    head = moe_layer_case(torch, dev, layers, T, args.steps, args.warmup, 3001)
+    a_bytes, b_bytes = head.pop("_stage_bytes")
+    value = head["gbs"]
 
-    uniq = np.array([len(np.unique(topk_ids(logits_h[i]))) for i in range(n_steps)])
-    step_bytes = uniq * EXPERT_BYTES + 2 * T * K * 2 + T * TOPK * 8 + T * E * 4
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        for Tc in (1, 4, 16):
+            if Tc == T:
+                continue
+            log(f"config 3 at T={Tc}")
+            c = moe_layer_case(torch, dev, layers, Tc, 20, 3, 3101 + Tc)
+            c.pop("_stage_bytes")
+            configs[f"cfg3_T{Tc}"] = c
+        log("routed dispatch (reference routing) at T=1")
+        configs["routed_dispatch_T1"] = routed_dispatch_case(torch, dev, layers, 20, 3)
 
-    def step(i: int):
-        return mods[i % L].forward(x, logits=logits[i])
-
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-    def timed(fn) -> float:
-        torch.cuda.synchronize()
-        ev0.record()
-        fn()
-        ev1.record()
-        torch.cuda.synchronize()
-        return ev0.elapsed_time(ev1)
-
-    log(f"warmup {args.warmup} steps, T={T}")
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # The K timed steps, captured once as a HIP graph (two kernels per step at
-    # T=1, three for T>1; no memsets) and replayed: the device-side cost of a
-    # decode loop whose host issues one graph launch. The same K steps issued
-    # eagerly are timed too.
-    log(f"capturing {args.steps} steps in a HIP graph")
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(args.warmup, n_steps):
-            step(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    log(f"timing {args.steps} steps (graph replay)")
-    ms_per_step_graph = timed(graph.replay) / args.steps
-    del graph
-    log(f"timing {args.steps} steps (issued from the host)")
-
-    def eager():
-        for i in range(args.warmup, n_steps):
-            step(i)
-
-    ms_per_step_host = timed(eager) / args.steps
-    ms_per_step = min(ms_per_step_host, ms_per_step_graph)
-    timed_bytes = float(step_bytes[args.warmup:].mean())
-    value = timed_bytes / (ms_per_step * 1e-3) / 1e9
-
-    # --- dominant kernel alone: stage A (W1/W3 + SiLU), back-to-back launches ---
-    R = min(64, n_steps)
-    stages = []
-    for i in range(R):
-        st = gb.MoEStages(layers[i % L].W1, layers[i % L].W3, layers[i % L].W2, T, TOPK, dev)
-        ids, w = gb.route_sigmoid_topk(logits[i], TOPK)
-        st.build_routing(ids, w)
-        stages.append(st)
-    out = torch.empty(T, O, dtype=torch.bfloat16, device=dev)
-    for st in stages:
-        st.swiglu(x)
-        st.down(out)
-    torch.cuda.synchronize()
-    ga, gbr = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-    with torch.cuda.graph(ga):
-        for st in stages:
-            st.swiglu(x)
-    with torch.cuda.graph(gbr):
-        for st in stages:
-            st.down(out)
-    ga.replay()
-    gbr.replay()
-    reps = max(1, args.steps // R)
-    log(f"timing stage A alone: {reps * R} launches (graph)")
-    a_us = timed(lambda: [ga.replay() for _ in range(reps)]) * 1e3 / (reps * R)
-    b_us = timed(lambda: [gbr.replay() for _ in range(reps)]) * 1e3 / (reps * R)
-    a_bytes = float(np.mean(uniq[:R] * STAGE_A_EXPERT_BYTES + T * K * 2 + T * TOPK * H * 2))
-    b_bytes = float(np.mean(uniq[:R] * STAGE_B_EXPERT_BYTES + T * TOPK * H * 2 + T * O * 2))
-    a_gbs = a_bytes / (a_us * 1e-6) / 1e9
-    b_gbs = b_bytes / (b_us * 1e-6) / 1e9
-    del ga, gbr, stages
-
-    # --- measured device-copy ceiling: torch's copy kernel over 1 GiB (read + write) ---
-    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    dst = torch.empty_like(src)
-    src.fill_(1)
-    dst.copy_(src)
-    copy_ms = timed(lambda: [dst.copy_(src) for _ in range(5)]) / 5
-    copy_gbs = 2 * src.numel() / (copy_ms * 1e-3) / 1e9
-    del src, dst
-
-    # --- CPU baseline: the oracle (dequant + fp32 matmul) on step 0's experts ---
     cpu = None
     if not args.no_cpu_baseline:
-        from threadpoolctl import threadpool_info, threadpool_limits
+        from runtime import synth
+        xh = torch.from_numpy(synth.normal_bf16(3001, (T, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+        lg0 = synth.gating_logits(3002, T, E)
+        cpu = cpu_baseline(torch, layers[0], xh, lg0, T, float(head["algorithmic_bytes_per_step"]))
 
-        from oracle import mx
-
-        ids0 = topk_ids(logits_h[0])
-        lw = layers[0]
-        cache = {}
-
-        def expert(e):
-            if e not in cache:
-                cache[e] = tuple((m["packed"][e].cpu().numpy(), m["scale"][e].cpu().numpy())
-                                 for m in (lw.W1, lw.W3, lw.W2))
-            return cache[e]
-
-        ids_t, w_t = mx.route_sigmoid_topk(logits_h[0], TOPK)
-        xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
-        for e in np.unique(ids_t):
-            expert(int(e))
-        threads = min(os.cpu_count() or 1, 16)
-        with threadpool_limits(limits=threads):
-            blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
-            log(f"cpu baseline: oracle moe layer, {threads} BLAS threads")
-            t0 = time.perf_counter()
-            n_calls = 0
-            while True:
-                mx.moe_layer(xh, expert, ids_t, w_t, O)
-                n_calls += 1
-                if time.perf_counter() - t0 > 10.0 or n_calls >= 3:
-                    break
-            cpu_s = (time.perf_counter() - t0) / n_calls
-            # (ii) the same layer with the weights dequantised ahead of time
-            dq = {int(e): mx.dequant_expert_f32(expert(int(e))) for e in np.unique(ids_t)}
-            t0 = time.perf_counter()
-            n_mm = 0
-            while True:
-                mx.moe_layer_dequantised(xh, dq.__getitem__, ids_t, w_t, O)
-                n_mm += 1
-                if time.perf_counter() - t0 > 5.0 or n_mm >= 20:
-                    break
-            mm_s = (time.perf_counter() - t0) / n_mm
-            del dq
-        cpu = {
-            "value": round(float(step_bytes[0]) / cpu_s / 1e9, 4),
-            "unit": "GB/s",
-            "us_per_layer": round(cpu_s * 1e6, 1),
-            "matmul_only_us_per_layer": round(mm_s * 1e6, 1),
-            "cores": int(blas[0]) if blas else threads,
-            "kind": "port",
-            "sample": (f"{n_calls} call(s) of the numpy oracle moe_layer (unpack + E8M0 scale -> "
-                       f"bf16 dequant, fp32 matmul, bf16 casts) on step 0: T={T}, "
-                       f"{len(np.unique(ids_t))} routed experts of layer 0; host {cpu_model()}, "
-                       f"nproc {os.cpu_count()}; matmul_only_us_per_layer: {n_mm} call(s) of "
-                       f"the same layer on weights dequantised to fp32 beforehand"),
-        }
-        del ids0
+    del layers
+    torch.cuda.empty_cache()
+    if configs is not None:
+        log(f"config 4: {args.c4_layers}-layer decode sweep and 512-token prefill")
+        c4 = config4_case(torch, dev, 8, 2, args.c4_layers)
+        configs["cfg4_decode"] = c4["decode"]
+        configs["cfg4_prefill"] = c4["prefill"]
 
     kernels = None
     if not args.no_kernels:
-        del layers, mods
-        torch.cuda.empty_cache()
-        log("per-kernel lines: dense MXFP4, FP8, RMSNorm")
+        log("per-kernel lines: dense MXFP4, FP8, RMSNorm, router")
         kernels = dense_kernels(torch, dev, cpu=not args.no_cpu_baseline)
 
-    # Counter passes are committed for T=1 and T=16; other T report null.
-    a_kernel = STAGE_A_KERNEL.get(T, STAGE_A_KERNEL_MULTI)
-    traffic, traffic_src = profiled_traffic(f"{a_kernel}@T{T}")
+    a_kernel = "moe_swiglu_t1_kernel_gated" if T == 1 else "moe_swiglu_tn_kernel"
+    b_kernel = "moe_down_t1_kernel" if T == 1 else "moe_down_tn_kernel"
+    a_us = head["stage_us"]["gate_swiglu_A"] if T == 1 else head["stage_us"]["swiglu_A_tables_given"]
+    b_us = head["stage_us"]["down_B"]
+    a_traffic, a_src = profiled_traffic(f"{a_kernel}@T{T}")
+    b_traffic, b_src = profiled_traffic(f"{b_kernel}@T{T}")
+
+    def roof(kernel, desc, us, nbytes, traffic, src):
+        return {"kernel": f"{kernel} ({desc})", "bound": "hbm", "achieved": round(gbs(nbytes, us), 2),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs(nbytes, us) / HBM_PEAK_GBS, 4),
+                "traffic": traffic, "traffic_source": src, "algorithmic_bytes_per_launch": int(round(nbytes)),
+                "avg_launch_us": round(us, 3)}
+
     result = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": value,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": round(head["moe_layer_us"] / 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -609,34 +745,33 @@ def main() -> int:
             "workload": f"configs[3]: routed MoE layer decode, T={T}, top-{TOPK} of {E} MXFP4 experts "
                         f"(W1/W3 {H}x{K}, W2 {O}x{H}), device sigmoid gating, {L} resident layers",
             "tokens": T, "experts": E, "topk": TOPK, "layers_cycled": L,
-            "mean_unique_experts": round(float(uniq[args.warmup:].mean()), 3),
-            "algorithmic_bytes_per_step": int(round(timed_bytes)),
+            "mean_unique_experts": head["mean_unique_experts"],
+            "algorithmic_bytes_per_step": head["algorithmic_bytes_per_step"],
         },
-        "timing": ("HIP graph replay" if ms_per_step_graph <= ms_per_step_host
-                   else "launches issued from the host loop")
-                  + " (the faster of the two over the same K steps; HIP events on the launch stream)",
-        "moe_layer_us": round(ms_per_step * 1e3, 3),
-        "moe_layer_us_graph": round(ms_per_step_graph * 1e3, 3),
-        "moe_layer_us_host_issued": round(ms_per_step_host * 1e3, 3),
-        "hbm_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-        "copy_ceiling_gbs": round(copy_gbs, 1),
-        "stage_us": {"swiglu_A": round(a_us, 3), "down_B": round(b_us, 3)},
-        "stage_gbs": {"swiglu_A": round(a_gbs, 1), "down_B": round(b_gbs, 1)},
-        "roofline": {
-            "kernel": f"{a_kernel} (stage A: W1+W3 MXFP4 GEMV + SiLU)",
-            "bound": "hbm",
-            "achieved": round(a_gbs, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(a_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_source": traffic_src,
-            "algorithmic_bytes_per_launch": int(round(a_bytes)),
-            "avg_launch_us": round(a_us, 3),
-        },
+        "timing": head["timing"] + " (the faster of the two over the same K steps; HIP events on the launch stream)",
+        "moe_layer_us": head["moe_layer_us"],
+        "moe_layer_us_graph": head["moe_layer_us_graph"],
+        "moe_layer_us_host_issued": head["moe_layer_us_host_issued"],
+        "hbm_frac_of_peak": head["hbm_frac_of_peak"],
+        "stage_us": head["stage_us"],
+        "stage_gbs": head["stage_gbs"],
+        "roofline": roof(a_kernel, "stage A of the timed step: gating + W1/W3 MXFP4 GEMV + SiLU" if T == 1
+                         else "stage A: W1/W3 MXFP4 GEMV + SiLU", a_us, a_bytes, a_traffic, a_src),
+        "stage_b_roofline": roof(b_kernel, "stage B: W2 MXFP4 GEMV + weighted combine", b_us, b_bytes,
+                                 b_traffic, b_src),
         "cpu_baseline": cpu,
+        "configs": configs,
         "kernels": kernels,
+        "bench_seconds": round(time.perf_counter() - t_start, 1),
     }
+    # the measured device-copy ceiling (torch's copy over 1 GiB, read + write)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    dst.copy_(src)
+    copy_ms = Timer(torch).ms(lambda: [dst.copy_(src) for _ in range(5)]) / 5
+    result["copy_ceiling_gbs"] = round(2 * src.numel() / (copy_ms * 1e-3) / 1e9, 1)
+    del src, dst
     print(json.dumps(result), flush=True)
     return 0
 

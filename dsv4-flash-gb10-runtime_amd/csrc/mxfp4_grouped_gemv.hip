@@ -1899,14 +1899,13 @@ int launch_router(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate, int T, int n_
     return 0;
 }
 
-// The routed layer from logits: gating (scored as `sc`) + stages A and B.
-// One token on the aligned path gates inside stage A (two launches).
-int moe_layer_impl(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_packed,
-                   const uint8_t* W3_packed, const uint8_t* W2_packed, const uint8_t* W1_scale,
-                   const uint8_t* W3_scale, const uint8_t* W2_scale, int T, int topk, int n_experts,
-                   int K_in, int hidden, int out_dim, dsv4_bf16_t* out, int32_t* ids_out,
-                   float* weights_out, const MoeCall& c, Scoring sc, hipStream_t stream) {
-    int v;
+// The first half of the routed layer from logits: gating (scored as `sc`)
+// and stage A. One token on the aligned path gates inside stage A (one
+// launch); otherwise the routing kernel runs first.
+int moe_gate_swiglu_impl(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_packed,
+                         const uint8_t* W3_packed, const uint8_t* W1_scale, const uint8_t* W3_scale, int T,
+                         int topk, int n_experts, int K_in, int hidden, int32_t* ids_out, float* weights_out,
+                         const MoeCall& c, Scoring sc, hipStream_t stream) {
     if (T == 1) {
         StageAArgs probe{};
         probe.K = K_in;
@@ -1916,14 +1915,22 @@ int moe_layer_impl(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_
         const bool al = aligned16(x) && aligned16(W1_packed) && aligned16(W3_packed);
         if (stage_a_t1_ok(probe, al)) {
             GateArgs g{logits, nullptr, nullptr, n_experts, topk, ids_out, weights_out, c.rt, sc};
-            v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
-            if (v != 0) return v;
-            return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
+            return launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream, &g);
         }
     }
-    v = launch_route(logits, nullptr, nullptr, T, topk, n_experts, ids_out, weights_out, c, stream, sc);
+    const int v = launch_route(logits, nullptr, nullptr, T, topk, n_experts, ids_out, weights_out, c, stream, sc);
     if (v != 0) return v;
-    v = launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
+    return launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
+}
+
+// The routed layer from logits: gating + stage A, then stage B.
+int moe_layer_impl(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_packed,
+                   const uint8_t* W3_packed, const uint8_t* W2_packed, const uint8_t* W1_scale,
+                   const uint8_t* W3_scale, const uint8_t* W2_scale, int T, int topk, int n_experts,
+                   int K_in, int hidden, int out_dim, dsv4_bf16_t* out, int32_t* ids_out,
+                   float* weights_out, const MoeCall& c, Scoring sc, hipStream_t stream) {
+    const int v = moe_gate_swiglu_impl(x, logits, W1_packed, W3_packed, W1_scale, W3_scale, T, topk, n_experts,
+                                       K_in, hidden, ids_out, weights_out, c, sc, stream);
     if (v != 0) return v;
     return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
 }
@@ -2090,6 +2097,18 @@ extern "C" int mxfp4_moe_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed,
     if (v != 0) return v;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     return launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
+}
+
+extern "C" int mxfp4_moe_gate_swiglu(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_packed,
+                                     const uint8_t* W3_packed, const uint8_t* W1_scale, const uint8_t* W3_scale,
+                                     int T, int topk, int n_experts, int K_in, int hidden, int32_t* ids_out,
+                                     float* weights_out, void* workspace, hipStream_t stream) {
+    const int v = moe_validate(T, topk, n_experts, K_in, hidden, 1);
+    if (v != 0) return v;
+    if (topk > n_experts) return -4;
+    const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
+    return moe_gate_swiglu_impl(x, logits, W1_packed, W3_packed, W1_scale, W3_scale, T, topk, n_experts, K_in,
+                                hidden, ids_out, weights_out, c, Scoring{kScoreSigmoid, 1.0f}, stream);
 }
 
 extern "C" int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale, int T, int topk,

@@ -80,6 +80,8 @@ def _load_lib() -> ctypes.CDLL:
     lib.mxfp4_moe_router_logits.argtypes = [_c_void_p] * 2 + [_c_int] * 3 + [_c_void_p] * 2
     lib.mxfp4_moe_dispatch_workspace_bytes.restype = _c_size_t
     lib.mxfp4_moe_dispatch_workspace_bytes.argtypes = [_c_int] * 4
+    lib.mxfp4_moe_gate_swiglu.restype = _c_int
+    lib.mxfp4_moe_gate_swiglu.argtypes = [_c_void_p] * 6 + [_c_int] * 5 + [_c_void_p] * 4
     lib.mxfp4_moe_grouped_gemv_noalloc.restype = _c_int
     lib.mxfp4_moe_grouped_gemv_noalloc.argtypes = ([_c_void_p] * 9 + [_c_int] * 6 + [_c_void_p] * 2)
     lib.mxfp4_moe_routed_dispatch.restype = _c_int
@@ -514,6 +516,17 @@ class MoEStages:
             _lib.vp(x), _lib.vp(self.W1["packed"]), _lib.vp(self.W3["packed"]),
             _lib.vp(self.W1["scale"]), _lib.vp(self.W3["scale"]), self.T, self.topk,
             self.n_experts, self.K, self.hidden, _lib.vp(self.workspace),
+            ctypes.c_void_p(_lib.stream_ptr(x.device))))
+
+    def gate_swiglu(self, x: torch.Tensor, logits: torch.Tensor, ids_out: Optional[torch.Tensor] = None,
+                    weights_out: Optional[torch.Tensor] = None) -> None:
+        """Gating of logits [T, E] and stage A (the first part of
+        mxfp4_moe_layer); down() completes the layer."""
+        self._rc("mxfp4_moe_gate_swiglu", self.lib.mxfp4_moe_gate_swiglu(
+            _lib.vp(x), _lib.vp(logits), _lib.vp(self.W1["packed"]), _lib.vp(self.W3["packed"]),
+            _lib.vp(self.W1["scale"]), _lib.vp(self.W3["scale"]), self.T, self.topk, self.n_experts, self.K,
+            self.hidden, None if ids_out is None else _lib.vp(ids_out),
+            None if weights_out is None else _lib.vp(weights_out), _lib.vp(self.workspace),
             ctypes.c_void_p(_lib.stream_ptr(x.device))))
 
     def down(self, out: torch.Tensor) -> torch.Tensor:

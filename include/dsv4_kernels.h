@@ -191,6 +191,16 @@ int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
                     dsv4_bf16_t* out, int32_t* ids_out, float* weights_out, void* workspace,
                     hipStream_t stream);
 
+/* EXTENSION: the first part of mxfp4_moe_layer (gating of logits and stage A,
+ * one launch for one token on the aligned path, two otherwise); followed by
+ * mxfp4_moe_down with the same workspace it completes the layer with the same
+ * bits. For callers that schedule the projections themselves and for
+ * per-launch timing. Arguments and return codes as mxfp4_moe_layer. */
+int mxfp4_moe_gate_swiglu(const dsv4_bf16_t* x, const float* logits, const uint8_t* W1_packed,
+                          const uint8_t* W3_packed, const uint8_t* W1_scale, const uint8_t* W3_scale,
+                          int T, int topk, int n_experts, int K_in, int hidden, int32_t* ids_out,
+                          float* weights_out, void* workspace, hipStream_t stream);
+
 /* EXTENSION: the reference's routed dispatch of one MoE layer on the device
  * (replaces dsv4_routed_dispatch, reference kernel/cpp-engine-mxfp4/routed.cu:373-503,
  * for T tokens): the router gate GEMV (mxfp4_moe_router_logits over x), the

@@ -22,7 +22,7 @@ LIBS = {
         "mxfp4_moe_build_routing", "mxfp4_moe_swiglu", "mxfp4_moe_down", "mxfp4_moe_layer",
         "mxfp4_moe_prefill_workspace_bytes", "mxfp4_moe_prefill", "mxfp4_moe_prefill_dequant_bf16",
         "mxfp4_moe_route_topk", "mxfp4_moe_router_logits", "mxfp4_moe_dispatch_workspace_bytes",
-        "mxfp4_moe_routed_dispatch", "mxfp4_moe_grouped_gemv_noalloc"],
+        "mxfp4_moe_routed_dispatch", "mxfp4_moe_grouped_gemv_noalloc", "mxfp4_moe_gate_swiglu"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
                                       "fp8_e4m3_gemv_multi",

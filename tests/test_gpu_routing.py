@@ -278,3 +278,24 @@ def test_routed_dispatch_config_shapes(device, cfg3_layer, T):
     # bit-deterministic across calls
     again = host_bits(gb.mxfp4_moe_routed_dispatch(xd, wgd, w.W1, w.W3, w.W2, k, 1.5))
     assert np.array_equal(again, out)
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_gate_swiglu_then_down_equals_layer(device, cfg3_layer, T):
+    """mxfp4_moe_gate_swiglu followed by mxfp4_moe_down (the bench's per-launch
+    timing split) gives the bits of mxfp4_moe_layer, with the same routing."""
+    w = cfg3_layer
+    announce(f"mxfp4_moe_gate_swiglu + mxfp4_moe_down T={T}")
+    x = dev_bf16(synth.normal_bf16(13400 + T, (T, K3)), device)
+    logits = dev_f32(synth.gating_logits(13410 + T, T, E3), device)
+    ids_a = torch.empty(T, 8, dtype=torch.int32, device=device)
+    w_a = torch.empty(T, 8, dtype=torch.float32, device=device)
+    st = gb.MoEStages(w.W1, w.W3, w.W2, T, 8, device)
+    st.gate_swiglu(x, logits, ids_a, w_a)
+    split = host_bits(st.down(torch.empty(T, O3, dtype=torch.bfloat16, device=device)))
+    ids_b = torch.empty(T, 8, dtype=torch.int32, device=device)
+    w_b = torch.empty(T, 8, dtype=torch.float32, device=device)
+    whole = host_bits(gb.mxfp4_moe_layer(x, logits, w.W1, w.W3, w.W2, 8, ids_out=ids_b, weights_out=w_b))
+    assert np.array_equal(split, whole)
+    assert np.array_equal(ids_a.cpu().numpy(), ids_b.cpu().numpy())
+    assert np.array_equal(w_a.cpu().numpy(), w_b.cpu().numpy())
