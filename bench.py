@@ -618,8 +618,10 @@ def cpu_baseline(torch, layer, x, logits_h, T: int, step_bytes: float) -> dict:
 def counters_run(torch, dev) -> int:
     """A short fixed sequence for rocprofv3 --pmc passes (no HIP graphs, a
     bounded number of dispatches): 24 one-token layers (gated stage A + stage
-    B) on 4 resident layers, 8 T=4 and 8 T=16 layers, then 32 launches of each
-    dense case. Kernel names identify the cases in the counter output."""
+    B) on 4 resident layers, 8 T=4 and 8 T=16 layers, two 512-token prefill
+    chunks, then 32 launches of each dense case and four 1 GiB copies (the
+    counters' calibration). Kernel names and grid sizes identify the cases in
+    the counter output."""
     from runtime import moe, synth
 
     layers = [moe.make_moe_weights(20000 + 100 * l, E, K, H, O, dev) for l in range(4)]
@@ -631,11 +633,29 @@ def counters_run(torch, dev) -> int:
             mods[i % 4].forward(x, logits=lg[i])
         torch.cuda.synchronize()
         log(f"counters: {n} layers at T={T}")
-    del layers
+    # one 512-token prefill chunk on each of two layers (MFMA grouped GEMM)
+    from runtime import mxfp4_grouped_gemv_binding as gb
+    TP = 512
+    xp = torch.from_numpy(synth.normal_bf16(4002, (TP, K)).view(np.int16)).view(torch.bfloat16).to(dev)
+    ws = torch.empty(gb.prefill_workspace_bytes(TP, TOPK, E, H, O), dtype=torch.uint8, device=dev)
+    for l in range(2):
+        ids, w = synth.zipf_routing(4003, TP, E, TOPK, 1.1, layer=l)
+        gb.mxfp4_moe_prefill(xp, layers[l].W1, layers[l].W3, layers[l].W2, torch.from_numpy(ids).to(dev),
+                             torch.from_numpy(w).to(dev), workspace=ws)
+    torch.cuda.synchronize()
+    log("counters: 2 prefill chunks of 512 tokens")
+    del layers, ws
     torch.cuda.empty_cache()
     dense_kernels(torch, dev, cpu=False, counters=True)
     torch.cuda.synchronize()
     log("counters: dense cases done")
+    # calibration: torch's copy kernel over 1 GiB (reads 1 GiB, writes 1 GiB)
+    src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("counters: calibration copies done")
     return 0
 
 
