@@ -313,6 +313,164 @@ __global__ __launch_bounds__(256) void fp8_gemv_multi_kernel(const MultiArgs ma)
     fp8_tile_body<C, TT, KC, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part);
 }
 
+// Two to sixteen tokens on the matrix cores (v_mfma_f32_16x16x32_bf16). On
+// the vector path every weight pair costs one v_dot2 per token, so at T = 8
+// the dots, not the weight stream, set the time; here one instruction takes
+// 16 rows x 32 k of weights against 32 k x 16 tokens.
+//   Workgroup: 16 rows (n0 .. n0+15) x all of K; NW waves split K, wave w
+//   owning k in [w*KW, (w+1)*KW), KW = 512*PASSES.
+//   Lane l: weight row r = l%16 and token column l%16 (clamped to T-1),
+//   k-group g = l/16. Per pass, load j (0..7) reads the 16 bytes
+//   k0 + 64j + 16g .. +15 of row r (one instruction covers 16 rows x 64 B)
+//   and the 16 activations at the same k; each half (8 k) is one MFMA
+//   operand, exact bf16 from E4M3. A 128-k scale tile is 2 loads; its 4
+//   MFMAs accumulate into a fresh fp32 tile sum, which is scaled and added.
+//   The D operand gives lane l rows 4g..4g+3 for token l%16; each row's tile
+//   scales come from the lane that loaded that row (ds_bpermute), so 16-row
+//   blocks may straddle a 128-row scale tile (groups starting mid-tile).
+//   The NW partial sums meet in LDS and are added in wave order.
+constexpr int kMmaLoads = 8;        // 16-byte weight loads per lane per pass
+constexpr int kMmaK = 64 * kMmaLoads;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 8 E4M3 bytes (two dwords) -> 8 bf16, element order kept.
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t d0, uint32_t d1) {
+    const bf16x2 p0 = fp8x2_to_bf16x2<false>(d0), p1 = fp8x2_to_bf16x2<true>(d0);
+    const bf16x2 p2 = fp8x2_to_bf16x2<false>(d1), p3 = fp8x2_to_bf16x2<true>(d1);
+    bf16x8 v;
+    v[0] = p0[0]; v[1] = p0[1]; v[2] = p1[0]; v[3] = p1[1];
+    v[4] = p2[0]; v[5] = p2[1]; v[6] = p3[0]; v[7] = p3[1];
+    return v;
+}
+
+template <int NW, int PASSES, int MAT>
+__device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
+                                              int blk, float (*part)[MAT][16][16]) {
+    constexpr int L = kMmaLoads;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int n0 = blk * 16;
+    const int64_t gn = gv.row0 + min(n0 + r, a.N - 1);
+    const uint16_t* xr = gv.x + (int64_t)min(r, a.T - 1) * a.xstride + 16 * g;
+    const uint8_t* wr[MAT];
+    const uint8_t* sr[MAT];
+    wr[0] = a.w + gn * a.wrow + 16 * g;
+    sr[0] = a.s + (gn / kTile) * a.srow;
+    if constexpr (MAT == 2) {
+        wr[1] = sw.w3 + gn * a.wrow + 16 * g;
+        sr[1] = sw.s3 + (gn / kTile) * a.srow;
+    }
+    f32x4 acc[MAT];
+#pragma unroll
+    for (int m = 0; m < MAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int k0 = (wave * PASSES + p) * kMmaK;
+        // This lane's row: the scale bytes of the pass's 4 k-tiles.
+        uint32_t s4[MAT];
+#pragma unroll
+        for (int m = 0; m < MAT; ++m) {
+            const uint8_t* sp = sr[m] + k0 / kTile;
+            s4[m] = (uint32_t)sp[0] | ((uint32_t)sp[1] << 8) | ((uint32_t)sp[2] << 16) | ((uint32_t)sp[3] << 24);
+        }
+        u32x4 xv[L][2];
+        u32x4 wv[MAT][L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const u32x4* x4 = reinterpret_cast<const u32x4*>(xr + k0 + 64 * j);
+            xv[j][0] = x4[0];
+            xv[j][1] = x4[1];
+#pragma unroll
+            for (int m = 0; m < MAT; ++m) wv[m][j] = ld16_stream(wr[m] + k0 + 64 * j);
+        }
+        // Every load of the pass is issued before the first multiply (loads
+        // complete in issue order, so each multiply waits only for its own).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < MAT; ++m) {
+            // Rows 4g..4g+3 of the D operand: their packed tile scales.
+            uint32_t srow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                srow[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m]);
+#pragma unroll
+            for (int tile = 0; tile < L / 2; ++tile) {
+                f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * tile + h;
+                    const bf16x8 a0 = fp8x8_to_bf16x8(wv[m][j][0], wv[m][j][1]);
+                    const bf16x8 a1 = fp8x8_to_bf16x8(wv[m][j][2], wv[m][j][3]);
+                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
+                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[m][i] = fmaf(ts[i], e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu), acc[m][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MAT; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][m][4 * g + i][r] = acc[m][i];
+    __syncthreads();
+    for (int o = t; o < 256; o += 64 * NW) {
+        const int tok = o >> 4;
+        const int row = o & 15;
+        if (tok >= a.T || n0 + row >= a.N) continue;
+        float sum[MAT];
+#pragma unroll
+        for (int m = 0; m < MAT; ++m) {
+            sum[m] = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) sum[m] += part[w2][m][row][tok];
+        }
+        uint16_t out;
+        if constexpr (MAT == 2) {
+            const float gt = swiglu_clamp(bf16_bits_to_f32(f32_to_bf16_bits(sum[0])), sw.limit);
+            const float u0 = bf16_bits_to_f32(f32_to_bf16_bits(sum[1]));
+            const float u = sw.clamp_up ? swiglu_clamp(u0, sw.limit) : u0;
+            out = f32_to_bf16_bits(gt / (1.0f + expf(-gt)) * u);
+        } else {
+            out = f32_to_bf16_bits(sum[0]);
+        }
+        gv.y[(int64_t)tok * a.ystride + n0 + row] = out;
+    }
+}
+
+// One matrix, or G row groups of one matrix (blockIdx.y); grid.x = ceil(N/16).
+template <int NW, int PASSES, int MAT>
+__global__ __launch_bounds__(64 * NW) void fp8_gemv_mfma_kernel(const Fp8Args a, const SwigluArgs sw) {
+    __shared__ float part[NW][MAT][16][16];
+    fp8_mfma_body<NW, PASSES, MAT>(a, sw, group_view(a), blockIdx.x, part);
+}
+
+// The matrices of fp8_e4m3_gemv_multi: matrix m owns workgroups
+// first[m] .. first[m+1]-1, 16 rows each.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const MultiArgs ma) {
+    __shared__ float part[NW][1][16][16];
+    int m = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxMulti; ++j) m += (j < ma.n_mats && (int)blockIdx.x >= ma.first[j]) ? 1 : 0;
+    Fp8Args a = ma.base;
+    a.w = ma.w[m];
+    a.s = ma.s[m];
+    a.N = ma.N[m];
+    a.wrow = ma.wrow[m];
+    a.srow = ma.srow[m];
+    a.y = ma.y[m];
+    a.ystride = ma.ystride[m];
+    const GroupView gv{a.x, a.y, 0};
+    fp8_mfma_body<NW, 1, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part);
+}
+
 // RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
 //   v = x + residual (fp32; or x alone), new_residual = bf16(v),
 //   x_norm = bf16( (g * bf16(v)) * rsqrt(sum(v^2) / K + eps) ),  y = W . x_norm
@@ -340,7 +498,9 @@ __device__ __forceinline__ void unpack8_f32(const u32x4 v, float* f) {
     }
 }
 
-template <int C, int TT, int KC, bool RESID>
+// GEMV = false: the norm alone (x_norm and new_residual, one workgroup); the
+// multi-token entry then runs the matrix-core GEMV on x_norm.
+template <int C, int TT, int KC, bool RESID, bool GEMV = true>
 __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a, const NormArgs nm) {
     constexpr int kRowsWG = C * 256 / KC;
     constexpr int kVals = C * TT;
@@ -377,11 +537,13 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
     __builtin_amdgcn_sched_barrier(0);
     u32x4 w[C];
     uint32_t sb[C];
+    if constexpr (GEMV) {
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-        const int64_t gn = min(n0 + (t + 256 * i) / KC, a.N - 1);
-        w[i] = ld16_stream(a.w + gn * a.wrow + k);
-        sb[i] = a.s[(gn / kTile) * a.srow + k / kTile];
+        for (int i = 0; i < C; ++i) {
+            const int64_t gn = min(n0 + (t + 256 * i) / KC, a.N - 1);
+            w[i] = ld16_stream(a.w + gn * a.wrow + k);
+            sb[i] = a.s[(gn / kTile) * a.srow + k / kTile];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -456,6 +618,7 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
         }
     }
 
+    if constexpr (!GEMV) return;
     float acc[kVals];
 #pragma unroll
     for (int i = 0; i < C; ++i) {
@@ -586,6 +749,52 @@ hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
     return hipGetLastError();
 }
 
+// The matrix-core path replaces the vector tile kernels once the per-token
+// dots outweigh its fixed costs. Its 16-row workgroups cover a matrix with
+// N/16 workgroups, and each wave load spans 16 rows x 64 B, so at small N or
+// few tokens the vector kernels (more workgroups, 1 KiB row loads) are
+// faster. Measured on MI355X over the MLA shapes (576, 1536, 4096 rows; K =
+// 1024 .. 8192; T = 1 .. 16): the matrix cores win from T = 4 at N >= 2048,
+// from T = 9 at N >= 1024, and from T = 2 at K = 8192. The rule looks at one
+// matrix's (or one group's) rows, so a grouped launch takes the path of a
+// single GEMV on each group.
+bool use_mfma(int T, int K, int N) {
+    if (T < 2) return false;
+    if (K > 4096) return true;
+    return (T >= 4 && N >= 2048) || (T > 8 && N >= 1024);
+}
+
+// The matrix-core path (T >= 2 on the tile shapes): NW waves of 512 k each,
+// except K = 8192 with two matrices (8 waves of two passes, which keeps the
+// second matrix's registers within the 1,024-thread workgroup's budget).
+template <int MAT>
+hipError_t launch_mfma(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)G);
+    switch (a.K) {
+        case 1024: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<2, 1, MAT>), grid, dim3(128), 0, stream, a, sw); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<4, 1, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 1, MAT>), grid, dim3(512), 0, stream, a, sw); break;
+        default:
+            if constexpr (MAT == 1)
+                hipLaunchKernelGGL((fp8_gemv_mfma_kernel<16, 1, 1>), grid, dim3(1024), 0, stream, a, sw);
+            else
+                hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 2, 2>), grid, dim3(512), 0, stream, a, sw);
+            break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_multi_mfma(const MultiArgs& ma, int blocks, hipStream_t stream) {
+    const dim3 grid((unsigned)blocks);
+    switch (ma.base.K) {
+        case 1024: hipLaunchKernelGGL((fp8_gemv_multi_mfma_kernel<2>), grid, dim3(128), 0, stream, ma); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_multi_mfma_kernel<4>), grid, dim3(256), 0, stream, ma); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_multi_mfma_kernel<8>), grid, dim3(512), 0, stream, ma); break;
+        default: hipLaunchKernelGGL((fp8_gemv_multi_mfma_kernel<16>), grid, dim3(1024), 0, stream, ma); break;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
     const dim3 grid((unsigned)blocks);
     switch (tile_tt(ma.base.T, ma.base.K, 1)) {
@@ -601,7 +810,8 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
 int launch(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
     if (tile_ok(a)) {
-        e = launch_tile<1>(a, SwigluArgs{}, G, stream);
+        e = use_mfma(a.T, a.K, a.N) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
+                                     : launch_tile<1>(a, SwigluArgs{}, G, stream);
     } else {
         const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);
         const dim3 block(64 * kWaves);
@@ -698,6 +908,8 @@ extern "C" int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, i
                       nullptr, 0, 0, 0};
     ma.n_mats = n_mats;
     bool tile = true;
+    bool mfma = true;
+    for (int m = 0; m < n_mats; ++m) mfma = mfma && use_mfma(T, K, N[m]);
     int blocks = 0;
     for (int m = 0; m < n_mats; ++m) {
         Fp8Args a = ma.base;
@@ -717,7 +929,8 @@ extern "C" int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, i
         ma.srow[m] = a.srow;
         ma.y[m] = a.y;
         ma.ystride[m] = a.ystride;
-        blocks += (N[m] + tile_rows(K) - 1) / tile_rows(K);
+        const int rows = mfma ? 16 : tile_rows(K);
+        blocks += (N[m] + rows - 1) / rows;
     }
     ma.first[n_mats] = blocks;
     if (!tile) {
@@ -736,7 +949,7 @@ extern "C" int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, i
         }
         return 0;
     }
-    const hipError_t e = launch_multi(ma, blocks, stream);
+    const hipError_t e = mfma ? launch_multi_mfma(ma, blocks, stream) : launch_multi(ma, blocks, stream);
     if (e != hipSuccess) {
         std::fprintf(stderr, "fp8_e4m3_gemv_multi launch failed: %s\n", hipGetErrorString(e));
         return -4;
@@ -764,7 +977,16 @@ extern "C" int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, 
         return -6;
     }
     const SwigluArgs sw{W3_fp8, W3_scale, limit, clamp_up};
-    // At most 8 tokens per launch (registers of the two matrices' partials).
+    if (use_mfma(T, K, N)) {
+        const hipError_t e = launch_mfma<2>(a, sw, 1, stream);
+        if (e != hipSuccess) {
+            std::fprintf(stderr, "fp8_e4m3_swiglu_gemv launch failed: %s\n", hipGetErrorString(e));
+            return -4;
+        }
+        return 0;
+    }
+    // Vector path: at most 8 tokens per launch (registers of the two
+    // matrices' partials).
     for (int t0 = 0; t0 < T; t0 += 8) {
         Fp8Args c = a;
         c.x = a.x + (int64_t)t0 * x_row_stride;
@@ -822,21 +1044,40 @@ extern "C" int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* re
     const NormArgs nm{reinterpret_cast<const uint16_t*>(residual), reinterpret_cast<const uint16_t*>(norm_weight),
                       eps, reinterpret_cast<uint16_t*>(x_norm), reinterpret_cast<uint16_t*>(new_residual)};
     const int KC = K / 16;
-    const dim3 grid((unsigned)((N + 4 * 256 / KC - 1) / (4 * 256 / KC)));
+    hipError_t e;
+    if (!use_mfma(T, K, N)) {
+        // One launch: the norm, then the GEMV slice of each workgroup.
+        const dim3 grid((unsigned)((N + 4 * 256 / KC - 1) / (4 * 256 / KC)));
 #define DSV4_NG(TTV, RES)                                                                                          \
     if (KC == 256) hipLaunchKernelGGL((fp8_norm_gemv_tile_kernel<4, TTV, 256, RES>), grid, dim3(256), 0, stream, a, nm); \
     else hipLaunchKernelGGL((fp8_norm_gemv_tile_kernel<4, TTV, 128, RES>), grid, dim3(256), 0, stream, a, nm);
-    if (residual) {
-        if (T == 1) { DSV4_NG(1, true) }
-        else if (T == 2) { DSV4_NG(2, true) }
-        else { DSV4_NG(4, true) }
-    } else {
-        if (T == 1) { DSV4_NG(1, false) }
-        else if (T == 2) { DSV4_NG(2, false) }
-        else { DSV4_NG(4, false) }
-    }
+        if (residual) {
+            if (T == 1) { DSV4_NG(1, true) }
+            else if (T == 2) { DSV4_NG(2, true) }
+            else { DSV4_NG(4, true) }
+        } else {
+            if (T == 1) { DSV4_NG(1, false) }
+            else if (T == 2) { DSV4_NG(2, false) }
+            else { DSV4_NG(4, false) }
+        }
 #undef DSV4_NG
-    const hipError_t e = hipGetLastError();
+        e = hipGetLastError();
+    } else {
+        // Where fp8_e4m3_gemv takes the matrix cores (here T = 4, N >= 2048):
+        // the norm in one workgroup, then that GEMV on x_norm (so y keeps its
+        // bits).
+#define DSV4_NO(KCV, RES) \
+    hipLaunchKernelGGL((fp8_norm_gemv_tile_kernel<4, 4, KCV, RES, false>), dim3(1), dim3(256), 0, stream, a, nm)
+        if (residual) { if (KC == 256) DSV4_NO(256, true); else DSV4_NO(128, true); }
+        else { if (KC == 256) DSV4_NO(256, false); else DSV4_NO(128, false); }
+#undef DSV4_NO
+        e = hipGetLastError();
+        if (e == hipSuccess) {
+            Fp8Args g = a;
+            g.x = reinterpret_cast<const uint16_t*>(x_norm);
+            e = launch_mfma<1>(g, SwigluArgs{}, 1, stream);
+        }
+    }
     if (e != hipSuccess) {
         std::fprintf(stderr, "fp8_e4m3_rmsnorm_gemv launch failed: %s\n", hipGetErrorString(e));
         return -4;

@@ -66,3 +66,73 @@ def test_fp8_swiglu_gemv_engine_k(device, N, K, T):
                                     dev_u8(s3, device), xd if T > 1 else xd[0], 10.0, False)
     assert_close(host_bits(act).reshape(T, N), mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, False),
                  f"fp8 swiglu N={N} K={K} T={T}")
+
+
+# Shapes on the matrix-core path (T >= 4 at N >= 2048, T > 8 at N >= 1024,
+# T >= 2 at K = 8192) next to the vector path at the same K: every K of the
+# tile set (2, 4, 8 and 16 waves per workgroup), a last 16-row block that is
+# partly past N, and K = 8192 with two matrices (two passes per wave).
+@pytest.mark.parametrize("N,K,T", [(2048, 1024, 8), (2050, 2048, 5), (4096, 2048, 4), (1100, 4096, 9),
+                                   (2048, 4096, 3), (4096, 8192, 16), (64, 8192, 2)])
+def test_fp8_matrix_core_path(device, N, K, T):
+    announce(f"fp8_e4m3_gemv matrix-core path N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(16000 + N + K, N, K)
+    x = synth.normal_bf16(16100 + T + K, (T, K))
+    y = fp8b.fp8_e4m3_gemv(dev_u8(w, device), dev_u8(s, device), dev_bf16(x, device))
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 N={N} K={K} T={T}")
+
+
+def test_fp8_matrix_core_groups_straddle_scale_tiles(device):
+    """Groups of 2056 rows: the second group starts 8 rows into a 16-row
+    block, so its blocks straddle 128-row scale tiles; each group's bits equal
+    a single GEMV on its slice (both on the matrix cores)."""
+    G, N, K, T = 2, 2056, 2048, 4
+    announce(f"fp8_e4m3_gemv_grouped matrix-core G={G} N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(16200, G * N, K)
+    x = synth.normal_bf16(16201, (T, G, K))
+    tw, ts = dev_u8(w, device), dev_u8(s, device)
+    xd = dev_bf16(x, device)
+    got = host_bits(fp8b.fp8_e4m3_gemv_grouped(tw, ts, xd, G)).reshape(T, G, N)
+    assert_close(got.reshape(T, -1), mx.fp8_gemv_grouped(x, w, s, G).reshape(T, -1), "grouped straddle")
+    # group 0 starts on a scale tile: its slice is a plain GEMV
+    y0 = fp8b.fp8_e4m3_gemv(tw[:N], ts[:(N + 127) // 128], xd[:, 0].contiguous())
+    assert np.array_equal(host_bits(y0).reshape(T, N), got[:, 0])
+
+
+@pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (2048, 4096, 8), (2048, 8192, 3), (1024, 2048, 12)])
+def test_fp8_swiglu_matrix_core(device, N, K, T):
+    """The fused SwiGLU on the matrix cores (K = 8192 runs two passes per
+    wave): against the oracle, and gate/up equal to the single GEMVs' bits."""
+    announce(f"fp8_e4m3_swiglu_gemv matrix-core N={N} K={K} T={T}")
+    w1, s1 = synth.fp8_weight(16300 + N + K, N, K)
+    w3, s3 = synth.fp8_weight(16400 + N + K, N, K)
+    x = mx.bf16_round(24 * mx.bf16_to_f32(synth.normal_bf16(16500 + T, (T, K))))
+    t1, u1, t3, u3 = dev_u8(w1, device), dev_u8(s1, device), dev_u8(w3, device), dev_u8(s3, device)
+    xd = dev_bf16(x, device)
+    act = host_bits(fp8b.fp8_e4m3_swiglu_gemv(t1, u1, t3, u3, xd, 10.0, True)).reshape(T, N)
+    gate = host_bits(fp8b.fp8_e4m3_gemv(t1, u1, xd)).reshape(T, N)
+    up = host_bits(fp8b.fp8_e4m3_gemv(t3, u3, xd)).reshape(T, N)
+    ref_bits = mx.swiglu_clamped(gate, up, 10.0, True)
+    diff = np.abs(act.astype(np.int32) - ref_bits.astype(np.int32))
+    diff[mx.bf16_to_f32(act) == mx.bf16_to_f32(ref_bits)] = 0
+    assert diff.max() <= 1, f"max bf16 ulp difference {diff.max()}"
+    assert_close(act, mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, True), f"swiglu matrix-core T={T}")
+
+
+def test_fp8_multi_matrix_core(device):
+    """Two matrices on the matrix cores in one launch: each output has the bits
+    of the single launch on that matrix."""
+    shapes, K, T = [4096, 2048], 4096, 8
+    announce(f"fp8_e4m3_gemv_multi matrix-core N={shapes} K={K} T={T}")
+    mats, dmats = [], []
+    for i, N in enumerate(shapes):
+        w, s = synth.fp8_weight(16600 + i, N, K)
+        mats.append((w, s))
+        dmats.append((dev_u8(w, device), dev_u8(s, device)))
+    x = synth.normal_bf16(16700, (T, K))
+    xd = dev_bf16(x, device)
+    ys = fp8b.fp8_e4m3_gemv_multi(dmats, xd)
+    for (w, s), (tw, ts), y, N in zip(mats, dmats, ys, shapes):
+        got = host_bits(y).reshape(T, N)
+        assert np.array_equal(got, host_bits(fp8b.fp8_e4m3_gemv(tw, ts, xd)).reshape(T, N))
+        assert_close(got, mx.fp8_gemv(x, w, s), f"multi matrix-core N={N}")
