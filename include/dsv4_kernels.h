@@ -291,7 +291,11 @@ int fp8_e4m3_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_fp8, const uint8_t* 
 /* EXTENSION (reference loops fp8_e4m3_gemv_m1 per token,
  * runtime/dsv4_engine_mxfp4.py:310-319): T-token FP8 GEMV that streams W once.
  * x [T, K] (row stride x_row_stride elements), y [T, N] (row stride
- * y_row_stride elements). Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16. */
+ * y_row_stride elements). With K in {1024, 2048, 4096, 8192} and 16-byte
+ * aligned operands it runs on the matrix cores (bf16 MFMA on the exact E4M3
+ * values) from T = 4 at N >= 2048, from T = 9 at N >= 1024 and from T = 2 at
+ * K = 8192, on the vector units otherwise; the two paths agree within fp32
+ * rounding of the sums. Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16. */
 int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
                   const uint8_t* W_scale, int K, int N, int T,
                   int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
@@ -304,8 +308,9 @@ int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_f
  *   y[t, g, n] = bf16( sum_k W[g*N + n, k] x[t, g, k] ),  g < G, n < N, t < T
  * with W [G*N, K] (scale rows (g*N+n)/128), x element (t, g, k) at
  * x + t*x_row_stride + g*x_group_stride + k, y element (t, g, n) at
- * y + t*y_row_stride + g*y_group_stride + n. Returns as fp8_e4m3_gemv, plus
- * -6 for G < 1 or G > 65535. */
+ * y + t*y_row_stride + g*y_group_stride + n. The path rule of fp8_e4m3_gemv
+ * applies to one group's N, so each group has the bits of fp8_e4m3_gemv on its
+ * slice. Returns as fp8_e4m3_gemv, plus -6 for G < 1 or G > 65535. */
 int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_group_stride,
                           const uint8_t* W_fp8, const uint8_t* W_scale, int G, int K, int N, int T,
                           int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
@@ -317,7 +322,9 @@ int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_
  * kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:395-418): n_mats GEMVs
  * that share x, K and T in one launch,
  *   y_m[t, n] = bf16( sum_k W_m[n, k] x[t, k] ),  n < N[m], m < n_mats,
- * with the bits fp8_e4m3_gemv writes for each matrix alone. The per-matrix
+ * with the bits fp8_e4m3_gemv writes for each matrix alone (the launch takes
+ * the matrix cores only when every matrix would alone; a matrix that would
+ * take them alone while another would not agrees within rounding). The per-matrix
  * arguments are host arrays of n_mats entries (pointers are device pointers):
  * W_fp8[m] [N[m], K] (row stride weight_row_stride_bytes[m]), W_scale[m]
  * [ceil(N[m]/128), K/128] (scale_row_stride_bytes[m]), y[m] [T, N[m]] (row
