@@ -575,6 +575,36 @@ def test_moe_prefill_small_vs_oracle(device, T, topk, E):
     assert np.array_equal(host_bits(again), host_bits(out))   # deterministic
 
 
+@pytest.mark.parametrize("K,H,O,T,topk,E", [(1024, 1024, 512, 40, 4, 16), (2048, 1024, 768, 40, 6, 24),
+                                             (4096, 2048, 256, 48, 8, 32)])
+def test_moe_prefill_mixed_tiles(device, K, H, O, T, topk, E):
+    """The prefill at K = 2048 and 4096 (the unrolled 16- and 32-super-step
+    bodies) and 1024 (the rolled body), with one expert of more than 16 pairs
+    (a tile of two or three token blocks) beside one-block tiles: against the oracle,
+    deterministic, with a dropped id and a duplicate listing."""
+    announce(f"mxfp4_moe_prefill mixed tiles T={T} topk={topk} E={E} K={K} H={H} O={O}")
+    W1p, W1s = synth.mxfp4_weight(8500 + K + E, H, K, E)
+    W3p, W3s = synth.mxfp4_weight(8504 + K + E, H, K, E)
+    W2p, W2s = synth.mxfp4_weight(8508 + K + E, O, H, E)
+    x = synth.normal_bf16(8510 + T, (T, K))
+    ids, w = mx.route_sigmoid_topk(synth.gating_logits(8520 + T, T, E), topk)
+    ids = ids.copy()
+    ids[0, 1] = ids[0, 0]
+    ids[T - 1, 0] = -1
+    ids[:T // 2, 0] = 3                # one expert with more than 16 pairs
+    counts = np.bincount(ids[ids >= 0].ravel(), minlength=E)
+    assert (counts > 16).any() and ((counts >= 1) & (counts <= 16)).any()
+    W1, W3, W2 = _dev_mats(device, W1p, W3p, W2p, W1s, W3s, W2s)
+    xd, idd, wd = dev_bf16(x, device), torch.from_numpy(ids).to(device), dev_f32(w, device)
+    out = host_bits(gb.mxfp4_moe_prefill(xd, W1, W3, W2, idd, wd))
+
+    def fn(e):
+        return (W1p[e], W1s[e]), (W3p[e], W3s[e]), (W2p[e], W2s[e])
+
+    assert_close(out, mx.moe_layer(x, fn, ids, w, O, n_experts=E), f"prefill mixed tiles K={K}")
+    assert np.array_equal(host_bits(gb.mxfp4_moe_prefill(xd, W1, W3, W2, idd, wd)), out)
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_moe_special_scale_bytes_decode(device, T):
     """The decode kernels (one-token and multi-token paths, K = 2048) with E8M0
