@@ -33,6 +33,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import re
 import os
 import platform
 import sys
@@ -542,7 +543,40 @@ def dense_kernels(torch, dev, cpu: bool, counters: bool = False) -> dict:
         out[f"rmsnorm_fuse_residual_add T={T}x{Hn}"] = entry(us, nb + 2 * Hn,
                                                              cpu_us(lambda: mx.rmsnorm_residual(h, r, g)))
         del Hc, Rc
+    add_traffic(out)
     return out
+
+
+def traffic_key(name: str):
+    """The `TRAFFIC` key of profiles/*.md for a dense-kernel line of the
+    bench (None for the reference-call-pattern comparison lines)."""
+    m = re.match(r"fp8_e4m3_gemv (?:wq_b |wo_b )?(\d+)x(\d+) T=(\d+)$", name)
+    if m:
+        return f"fp8_gemv_{m.group(1)}x{m.group(2)}@T{m.group(3)}"
+    m = re.match(r"rmsnorm_fuse_residual_add T=(\d+)x\d+$", name)
+    if m:
+        return f"rmsnorm_fuse_residual_add@T{m.group(1)}"
+    fixed = {"mxfp4_gemv_m1 2048x4096": "mxfp4_gemv_m1@T1",
+             "fp8_e4m3_gemv_multi wq_a 1024x4096 + wkv 512x4096 T=1": "fp8_gemv_multi_wqa_wkv@T1",
+             "fp8_e4m3_gemv_grouped wo_a 8x1024x4096 T=1": "fp8_gemv_grouped_wo_a@T1",
+             "fp8_e4m3_swiglu_gemv shared expert 2x2048x4096 T=1": "fp8_swiglu_gemv@T1",
+             "fp8_e4m3_rmsnorm_gemv residual+norm+wq_a 1536x4096 T=1": "fp8_rmsnorm_gemv@T1",
+             "router_logits bf16 256x4096 T=1": "router_logits@T1"}
+    return fixed.get(name)
+
+
+def add_traffic(kernels: dict) -> None:
+    """Attach the rocprof-measured HBM bytes per launch (profiles/*.md) and
+    the GB/s they make at the measured time to each dense-kernel line."""
+    for name, e in kernels.items():
+        key = traffic_key(name)
+        if key is None or not e.get("us"):
+            continue
+        tb, src = profiled_traffic(key)
+        if tb is not None:
+            e["traffic_bytes"] = tb
+            e["traffic_gbs"] = round(gbs(tb, e["us"]), 1)
+            e["traffic_source"] = src
 
 
 # ----------------------------------------------------------- CPU baseline ---
@@ -711,6 +745,18 @@ def main() -> int:
             log(f"config 3 at T={Tc}")
             c = moe_layer_case(torch, dev, layers, Tc, 20, 3, 3101 + Tc)
             c.pop("_stage_bytes")
+            # rocprof HBM bytes per launch of the stage kernels (profiles/*.md)
+            kn = ("moe_swiglu_t1_kernel_gated", "moe_down_t1_kernel") if Tc == 1 else \
+                ("moe_swiglu_tn_kernel", "moe_down_tn_kernel")
+            st = {}
+            for stage, kname, us_key in (("A", kn[0], "swiglu_A_tables_given" if Tc > 1 else "gate_swiglu_A"),
+                                         ("B", kn[1], "down_B")):
+                tb, src = profiled_traffic(f"{kname}@T{Tc}")
+                if tb is not None:
+                    st[stage] = {"kernel": kname, "traffic_bytes": tb, "source": src,
+                                 "traffic_gbs": round(gbs(tb, c["stage_us"][us_key]), 1)}
+            if st:
+                c["stage_traffic"] = st
             configs[f"cfg3_T{Tc}"] = c
         log("routed dispatch (reference routing) at T=1")
         configs["routed_dispatch_T1"] = routed_dispatch_case(torch, dev, layers, 20, 3)
