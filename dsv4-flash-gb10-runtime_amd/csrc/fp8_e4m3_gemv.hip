@@ -693,8 +693,15 @@ bool tile_ok(const Fp8Args& a) {
            (a.xgroup % 8 == 0) && tile_k(a.K);
 }
 
-// Rows per workgroup of the tile kernels: four chunks per thread.
-int tile_rows(int K) { return 4 * 256 / (K / 16); }
+// Chunks per thread of the vector tile kernels: two up to K = 4096 (twice
+// the workgroups of four, which measured 2-14% faster at the MLA shapes,
+// most at small N and several tokens), four at K = 8192 (two k-slices per
+// thread; two chunks there measured 8% slower). A row's chunks are reduced
+// by the same lanes and waves either way, so the results do not depend on it.
+constexpr int tile_c(int K) { return K > 4096 ? 4 : 2; }
+
+// Rows per workgroup of the tile kernels.
+int tile_rows(int K) { return tile_c(K) * 256 / (K / 16); }
 
 // Tokens per group: all of them up to 16 (8 with two matrices), at most 4 per
 // group with two k-slices per thread (K = 8192), which hold twice the
@@ -710,12 +717,12 @@ int tile_tt(int T, int K, int MAT) {
 template <int TT, int MAT>
 void launch_tile_tt(const Fp8Args& a, const SwigluArgs& sw, dim3 grid, hipStream_t stream) {
     switch (a.K) {
-        case 1024: hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 64, MAT>), grid, dim3(256), 0, stream, a, sw); break;
-        case 2048: hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 128, MAT>), grid, dim3(256), 0, stream, a, sw); break;
-        case 4096: hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 256, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 1024: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(1024), TT, 64, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(2048), TT, 128, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(4096), TT, 256, MAT>), grid, dim3(256), 0, stream, a, sw); break;
         default:
             if constexpr (TT <= 4)
-                hipLaunchKernelGGL((fp8_gemv_tile_kernel<4, TT, 512, MAT>), grid, dim3(256), 0, stream, a, sw);
+                hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(8192), TT, 512, MAT>), grid, dim3(256), 0, stream, a, sw);
             break;
     }
 }
@@ -723,12 +730,12 @@ void launch_tile_tt(const Fp8Args& a, const SwigluArgs& sw, dim3 grid, hipStream
 template <int TT>
 void launch_multi_tt(const MultiArgs& ma, dim3 grid, hipStream_t stream) {
     switch (ma.base.K) {
-        case 1024: hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 64>), grid, dim3(256), 0, stream, ma); break;
-        case 2048: hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 128>), grid, dim3(256), 0, stream, ma); break;
-        case 4096: hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 256>), grid, dim3(256), 0, stream, ma); break;
+        case 1024: hipLaunchKernelGGL((fp8_gemv_multi_kernel<tile_c(1024), TT, 64>), grid, dim3(256), 0, stream, ma); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_multi_kernel<tile_c(2048), TT, 128>), grid, dim3(256), 0, stream, ma); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_multi_kernel<tile_c(4096), TT, 256>), grid, dim3(256), 0, stream, ma); break;
         default:
             if constexpr (TT <= 4)
-                hipLaunchKernelGGL((fp8_gemv_multi_kernel<4, TT, 512>), grid, dim3(256), 0, stream, ma);
+                hipLaunchKernelGGL((fp8_gemv_multi_kernel<tile_c(8192), TT, 512>), grid, dim3(256), 0, stream, ma);
             break;
     }
 }
