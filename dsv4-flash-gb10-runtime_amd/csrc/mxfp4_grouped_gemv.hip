@@ -1567,8 +1567,10 @@ __global__ __launch_bounds__(64) void moe_route_topk_kernel(const float* logits,
 // registers while the T tokens' activation pieces (L2 hits after the first
 // wave) are dotted against them with v_dot2_f32_bf16; the lane sums are
 // reduced over the wave. Pieces past the row (K not a multiple of 512) are
-// loaded clamped and multiplied by zero activations.
-constexpr int kRouterWaves = 4;
+// loaded clamped and multiplied by zero activations. One wave per workgroup
+// (256 workgroups for 256 experts): 3.14 µs for 256 x 4096 against 3.21 with
+// two waves and 3.42 with four.
+constexpr int kRouterWaves = 1;
 
 template <int NJ>
 __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_gemv_kernel(const uint16_t* x, const uint16_t* wg,
