@@ -2,14 +2,18 @@
 //
 //   y[t,n] = bf16( sum_k e4m3(W[n,k]) * 2^(S[n/128,k/128]-127) * x[t,k] )
 //
-// Wave layout: lane l owns the 16-byte chunks k = 1024*j + 16*l of every row
-// it visits (one wave-wide load = 1 KiB of a row, coalesced), so each chunk
-// lies inside one 128-column scale tile. E4M3FN bytes are decoded with
-// v_cvt_scalef32_pk_bf16_fp8 (OCP e4m3fn on gfx950, exact in bf16),
-// multiplied against the bf16 activation pairs with v_dot2_f32_bf16 in fp32,
-// and the tile scale is applied once per chunk. kRows rows per wave are
-// reduced together with one butterfly. N need not be a multiple of 128
-// (ceil(N/128) scale rows), unlike reference kernel/fp8-dense/fp8_e4m3_gemv.cu:148-154.
+// Three kernels share the decode (v_cvt_scalef32_pk_bf16_fp8: OCP e4m3fn
+// on gfx950, exact in bf16) and the scale rule (the 128x128 tile scale is
+// applied once per 16-byte chunk or 128-k tile sum):
+//   - the general kernel (any K, unaligned operands): lane l owns the
+//     16-byte chunks k = 1024*j + 16*l of every row it visits, kRows rows
+//     per wave reduced together with one butterfly;
+//   - the vector tile kernels (K in {1024, 2048, 4096, 8192}, aligned): one
+//     wave instruction reads 1 KiB of one row, v_dot2_f32_bf16 per token;
+//   - the matrix-core kernel for several tokens (v_mfma_f32_16x16x32_bf16),
+//     taken by the shape rule use_mfma.
+// N need not be a multiple of 128 (ceil(N/128) scale rows), unlike reference
+// kernel/fp8-dense/fp8_e4m3_gemv.cu:148-154.
 
 #include <cstdio>
 
