@@ -251,6 +251,71 @@ def test_moe_layer_gated_sqrt_softplus_one_token(device, name, logits, k):
     torch.cuda.empty_cache()
 
 
+def _multi_token_gating_cases():
+    """Logit sets for the layer's gating of several tokens:
+    shared and identical tokens (many pairs per slot), ties, signed zeros,
+    -inf (with a row of all -inf), NaN, the most entries (T = 16, top-16 of
+    1024 experts) and every expert routed (E = 8)."""
+    rng = np.random.default_rng(13500)
+    cases = []
+    sh = rng.standard_normal((16, 256)).astype(np.float32)
+    sh[::2, 3] += 8.0
+    sh[::2, 200] += 8.0
+    cases.append(("shared experts", sh, 8))
+    cases.append(("identical tokens", np.tile(rng.standard_normal((1, 256)), (16, 1)), 8))
+    cases.append(("halves", np.round(rng.standard_normal((5, 256)) * 2) / 2, 8))
+    z = np.zeros((4, 256), dtype=np.float32)
+    z[:, ::3] = -0.0
+    z[0, [7, 90, 200]] = [1.0, 2.0, 1.0]
+    z[1, 250] = -1.0
+    z[2] = np.round(rng.standard_normal(256))
+    cases.append(("signed zeros", z, 8))
+    ni = np.full((3, 256), -np.inf, dtype=np.float32)
+    ni[0, [3, 77, 130]] = [0.5, -2.0, 0.5]
+    ni[2] = rng.standard_normal(256)
+    cases.append(("minus inf", ni, 8))
+    na = rng.standard_normal((3, 256)).astype(np.float32)
+    na[:, 1::4] = np.nan
+    cases.append(("nan entries", na, 8))
+    cases.append(("E=1024 k=16 T=16", np.round(rng.standard_normal((16, 1024)) * 4) / 4, 16))
+    cases.append(("E=200 k=16 T=9", rng.standard_normal((9, 200)), 16))
+    cases.append(("E=300 k=5 T=7", rng.standard_normal((7, 300)), 5))
+    cases.append(("E=8 k=8 T=2", rng.standard_normal((2, 8)), 8))
+    return cases
+
+
+@pytest.mark.parametrize("name,logits,k", _multi_token_gating_cases(),
+                         ids=lambda v: v if isinstance(v, str) else "")
+def test_moe_layer_multi_token_gating(device, name, logits, k):
+    """The layer of 2 to 16 tokens gates on the device (the routing kernel
+    ranks the logits, then stage A and stage B): the ids equal the oracle's,
+    the weights agree to float rounding, the output matches the oracle on
+    those ids, and its bits equal those of the grouped GEMV given the
+    published ids and weights (the routing kernel's ids path)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    K, H, O = 2048, (32 if E > 256 else 64), 128
+    announce(f"mxfp4_moe_layer gating in stage A: {name} T={T} E={E} k={k} K={K} H={H} O={O}")
+    w = moe.make_moe_weights(13600 + E, E, K, H, O, device)
+    x = synth.normal_bf16(13700 + T, (T, K))
+    xd = dev_bf16(x, device)
+    ids_out = torch.empty(T, k, dtype=torch.int32, device=device)
+    w_out = torch.empty(T, k, dtype=torch.float32, device=device)
+    out = host_bits(gb.mxfp4_moe_layer(xd, dev_f32(logits, device), w.W1, w.W3, w.W2, k,
+                                       ids_out=ids_out, weights_out=w_out))
+    rids, rw = mx.route_sigmoid_topk(logits, k)
+    assert np.array_equal(ids_out.cpu().numpy(), rids), name
+    # a row whose logits are all -inf gets 0/0 weights in both
+    assert np.allclose(w_out.cpu().numpy(), rw, rtol=1e-5, atol=1e-6, equal_nan=True), name
+    routed = host_bits(gb.mxfp4_moe_grouped_gemv(xd, w.W1, w.W3, w.W2, ids_out, w_out))
+    assert np.array_equal(out, routed), f"{name}: gated layer differs from the routing kernel's path"
+    rows = np.all(np.isfinite(rw), axis=1)
+    ref = mx.moe_layer(x[rows], _host_expert_fn(w), rids[rows], rw[rows], O, n_experts=E)
+    assert_close(out[rows], ref, name)
+    del w
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_routed_dispatch_config_shapes(device, cfg3_layer, T):
     """The reference engine's routed dispatch at its shapes (256 experts,
