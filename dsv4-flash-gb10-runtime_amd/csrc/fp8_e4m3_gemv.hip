@@ -321,18 +321,19 @@ __global__ __launch_bounds__(256) void fp8_gemv_multi_kernel(const MultiArgs ma)
 // the vector path every weight pair costs one v_dot2 per token, so at T = 8
 // the dots, not the weight stream, set the time; here one instruction takes
 // 16 rows x 32 k of weights against 32 k x 16 tokens.
-//   Workgroup: 16 rows (n0 .. n0+15) x all of K; NW waves split K, wave w
-//   owning k in [w*KW, (w+1)*KW), KW = 512*PASSES.
-//   Lane l: weight row r = l%16 and token column l%16 (clamped to T-1),
-//   k-group g = l/16. Per pass, load j (0..7) reads the 16 bytes
-//   k0 + 64j + 16g .. +15 of row r (one instruction covers 16 rows x 64 B)
-//   and the 16 activations at the same k; each half (8 k) is one MFMA
-//   operand, exact bf16 from E4M3. A 128-k scale tile is 2 loads; its 4
-//   MFMAs accumulate into a fresh fp32 tile sum, which is scaled and added.
-//   The D operand gives lane l rows 4g..4g+3 for token l%16; each row's tile
-//   scales come from the lane that loaded that row (ds_bpermute), so 16-row
-//   blocks may straddle a 128-row scale tile (groups starting mid-tile).
-//   The NW partial sums meet in LDS and are added in wave order.
+//   Workgroup: R blocks of 16 rows (n0 .. n0+16R-1) x all of K; NW waves
+//   split K, wave w owning k in [w*KW, (w+1)*KW), KW = 512*PASSES.
+//   Lane l: row r = l%16 of each block and token column l%16, k-group
+//   g = l/16. Per pass, load j (0..7) reads the 16 bytes k0 + 64j + 16g ..
+//   +15 of row r of each block (one instruction covers 16 rows x 64 B) and
+//   the activations of token l%16 at the same k (token columns T..15 read
+//   zeros); each half (8 k) is one MFMA operand, exact bf16 from E4M3. The
+//   R blocks share the activation registers. A 128-k scale tile is 2 loads;
+//   its 4 MFMAs accumulate into a fresh fp32 tile sum, which is scaled and
+//   added. The D operand gives lane l rows 4g..4g+3 for token l%16; each
+//   row's tile scales come from the lane that loaded that row (ds_bpermute),
+//   so 16-row blocks may straddle a 128-row scale tile (groups starting
+//   mid-tile). The NW partial sums meet in LDS and are added in wave order.
 constexpr int kMmaLoads = 8;        // 16-byte weight loads per lane per pass
 constexpr int kMmaK = 64 * kMmaLoads;
 
@@ -349,84 +350,102 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t d0, uint32_t d1) {
     return v;
 }
 
-template <int NW, int PASSES, int MAT>
+template <int NW, int PASSES, int MAT, int R>
 __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
-                                              int blk, float (*part)[MAT][16][16]) {
+                                              int blk, float (*part)[MAT][16 * R][16]) {
     constexpr int L = kMmaLoads;
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
     const int r = lane & 15;
     const int g = lane >> 4;
-    const int n0 = blk * 16;
-    const int64_t gn = gv.row0 + min(n0 + r, a.N - 1);
-    const uint16_t* xr = gv.x + (int64_t)min(r, a.T - 1) * a.xstride + 16 * g;
-    const uint8_t* wr[MAT];
-    const uint8_t* sr[MAT];
-    wr[0] = a.w + gn * a.wrow + 16 * g;
-    sr[0] = a.s + (gn / kTile) * a.srow;
-    if constexpr (MAT == 2) {
-        wr[1] = sw.w3 + gn * a.wrow + 16 * g;
-        sr[1] = sw.s3 + (gn / kTile) * a.srow;
-    }
-    f32x4 acc[MAT];
+    const int n0 = blk * 16 * R;
+    // Activations through a buffer bounded at the T token rows: the lanes of
+    // token columns T..15 read zeros without touching memory (their outputs
+    // are dropped), so x costs T rows of loads, not 16.
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)gv.x, (short)0, (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2), 0x00020000);
+    const int xoff = (int)(((int64_t)r * a.xstride + 16 * g) * 2);
+    const uint8_t* wr[MAT][R];
+    const uint8_t* sr[MAT][R];
 #pragma unroll
-    for (int m = 0; m < MAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < R; ++b) {
+        const int64_t gn = gv.row0 + min(n0 + 16 * b + r, a.N - 1);
+        wr[0][b] = a.w + gn * a.wrow + 16 * g;
+        sr[0][b] = a.s + (gn / kTile) * a.srow;
+        if constexpr (MAT == 2) {
+            wr[1][b] = sw.w3 + gn * a.wrow + 16 * g;
+            sr[1][b] = sw.s3 + (gn / kTile) * a.srow;
+        }
+    }
+    f32x4 acc[MAT][R];
+#pragma unroll
+    for (int m = 0; m < MAT; ++m)
+#pragma unroll
+        for (int b = 0; b < R; ++b) acc[m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int k0 = (wave * PASSES + p) * kMmaK;
-        // This lane's row: the scale bytes of the pass's 4 k-tiles.
-        uint32_t s4[MAT];
+        // This lane's rows: the scale bytes of the pass's 4 k-tiles.
+        uint32_t s4[MAT][R];
 #pragma unroll
-        for (int m = 0; m < MAT; ++m) {
-            const uint8_t* sp = sr[m] + k0 / kTile;
-            s4[m] = (uint32_t)sp[0] | ((uint32_t)sp[1] << 8) | ((uint32_t)sp[2] << 16) | ((uint32_t)sp[3] << 24);
-        }
+        for (int m = 0; m < MAT; ++m)
+#pragma unroll
+            for (int b = 0; b < R; ++b) {
+                const uint8_t* sp = sr[m][b] + k0 / kTile;
+                s4[m][b] = (uint32_t)sp[0] | ((uint32_t)sp[1] << 8) | ((uint32_t)sp[2] << 16) |
+                           ((uint32_t)sp[3] << 24);
+            }
         u32x4 xv[L][2];
-        u32x4 wv[MAT][L];
+        u32x4 wv[MAT][R][L];
 #pragma unroll
         for (int j = 0; j < L; ++j) {
-            const u32x4* x4 = reinterpret_cast<const u32x4*>(xr + k0 + 64 * j);
-            xv[j][0] = x4[0];
-            xv[j][1] = x4[1];
+            xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + (k0 + 64 * j) * 2, 0, 0);
+            xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + (k0 + 64 * j) * 2 + 16, 0, 0);
 #pragma unroll
-            for (int m = 0; m < MAT; ++m) wv[m][j] = ld16_stream(wr[m] + k0 + 64 * j);
+            for (int b = 0; b < R; ++b)
+#pragma unroll
+                for (int m = 0; m < MAT; ++m) wv[m][b][j] = ld16_stream(wr[m][b] + k0 + 64 * j);
         }
         // Every load of the pass is issued before the first multiply (loads
         // complete in issue order, so each multiply waits only for its own).
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int m = 0; m < MAT; ++m) {
-            // Rows 4g..4g+3 of the D operand: their packed tile scales.
-            uint32_t srow[4];
+        for (int b = 0; b < R; ++b)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                srow[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m]);
-#pragma unroll
-            for (int tile = 0; tile < L / 2; ++tile) {
-                f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int j = 2 * tile + h;
-                    const bf16x8 a0 = fp8x8_to_bf16x8(wv[m][j][0], wv[m][j][1]);
-                    const bf16x8 a1 = fp8x8_to_bf16x8(wv[m][j][2], wv[m][j][3]);
-                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
-                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
-                }
+            for (int m = 0; m < MAT; ++m) {
+                // Rows 4g..4g+3 of the block's D operand: their packed tile scales.
+                uint32_t srow[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[m][i] = fmaf(ts[i], e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu), acc[m][i]);
+                    srow[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m][b]);
+#pragma unroll
+                for (int tile = 0; tile < L / 2; ++tile) {
+                    f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int j = 2 * tile + h;
+                        const bf16x8 a0 = fp8x8_to_bf16x8(wv[m][b][j][0], wv[m][b][j][1]);
+                        const bf16x8 a1 = fp8x8_to_bf16x8(wv[m][b][j][2], wv[m][b][j][3]);
+                        ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
+                        ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[m][b][i] = fmaf(ts[i], e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu), acc[m][b][i]);
+                }
             }
-        }
     }
 #pragma unroll
     for (int m = 0; m < MAT; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part[wave][m][4 * g + i][r] = acc[m][i];
+        for (int b = 0; b < R; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) part[wave][m][16 * b + 4 * g + i][r] = acc[m][b][i];
     __syncthreads();
-    for (int o = t; o < 256; o += 64 * NW) {
-        const int tok = o >> 4;
-        const int row = o & 15;
+    for (int o = t; o < 256 * R; o += 64 * NW) {
+        const int tok = o / (16 * R);
+        const int row = o % (16 * R);
         if (tok >= a.T || n0 + row >= a.N) continue;
         float sum[MAT];
 #pragma unroll
@@ -448,11 +467,11 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
     }
 }
 
-// One matrix, or G row groups of one matrix (blockIdx.y); grid.x = ceil(N/16).
-template <int NW, int PASSES, int MAT>
+// One matrix, or G row groups of one matrix (blockIdx.y); grid.x = ceil(N/(16R)).
+template <int NW, int PASSES, int MAT, int R>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_mfma_kernel(const Fp8Args a, const SwigluArgs sw) {
-    __shared__ float part[NW][MAT][16][16];
-    fp8_mfma_body<NW, PASSES, MAT>(a, sw, group_view(a), blockIdx.x, part);
+    __shared__ float part[NW][MAT][16 * R][16];
+    fp8_mfma_body<NW, PASSES, MAT, R>(a, sw, group_view(a), blockIdx.x, part);
 }
 
 // The matrices of fp8_e4m3_gemv_multi: matrix m owns workgroups
@@ -472,7 +491,7 @@ __global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const Mult
     a.y = ma.y[m];
     a.ystride = ma.ystride[m];
     const GroupView gv{a.x, a.y, 0};
-    fp8_mfma_body<NW, 1, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part);
+    fp8_mfma_body<NW, 1, 1, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part);
 }
 
 // RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
@@ -769,8 +788,10 @@ hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
 // from T = 9 at N >= 1024, and from T = 2 at K = 8192. The rule looks at one
 // matrix's (or one group's) rows, so a grouped launch takes the path of a
 // single GEMV on each group.
-bool use_mfma(int T, int K, int N) {
-    if (T < 2) return false;
+// The matrix-core kernel reads the T activation rows through one buffer
+// resource, whose byte extent must fit 31 bits.
+bool use_mfma(int T, int K, int N, int64_t xstride) {
+    if (T < 2 || ((int64_t)(T - 1) * xstride + K) * 2 > INT32_MAX) return false;
     if (K > 4096) return true;
     return (T >= 4 && N >= 2048) || (T > 8 && N >= 1024);
 }
@@ -778,19 +799,55 @@ bool use_mfma(int T, int K, int N) {
 // The matrix-core path (T >= 2 on the tile shapes): NW waves of 512 k each,
 // except K = 8192 with two matrices (8 waves of two passes, which keeps the
 // second matrix's registers within the 1,024-thread workgroup's budget).
+template <int MAT, int R>
+void launch_mfma_r(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R)), (unsigned)G);
+    switch (a.K) {
+        case 1024: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<2, 1, MAT, R>), grid, dim3(128), 0, stream, a, sw); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<4, 1, MAT, R>), grid, dim3(256), 0, stream, a, sw); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 1, MAT, R>), grid, dim3(512), 0, stream, a, sw); break;
+        default:  // K = 8192, R = 1 only
+            if constexpr (R == 1) {
+                if constexpr (MAT == 1)
+                    hipLaunchKernelGGL((fp8_gemv_mfma_kernel<16, 1, 1, 1>), grid, dim3(1024), 0, stream, a, sw);
+                else
+                    hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 2, 2, 1>), grid, dim3(512), 0, stream, a, sw);
+            }
+            break;
+    }
+}
+
+// Row blocks per wave (R): a wave multiplies R 16-row blocks against one set
+// of activation registers, so R divides the activation loads per weight byte
+// (at T = 16 they are twice the weight loads with R = 1). It also divides the
+// workgroups, and those must still cover the GPU: for K <= 4096, R = 2 or 4
+// is taken from T = 8 on when it leaves at least 256 workgroups (one per CU)
+// and 512 * R waves. Measured on MI355X for N = 4096 .. 32768, K = 1024 ..
+// 4096, T = 4, 8, 16: every 4096-row shape and 8192 x 1024 stay at R = 1;
+// 8192 x {2048, 4096}, 16384 x {1024, 2048} and 32768 x 1024 take R = 2
+// (9-17% faster at T = 16, e.g. 32768 x 1024: 13.9 -> 11.6 us); 16384 x
+// 4096 takes R = 4 (18% at T = 16). Each row's sums are formed in the same
+// order for every R, so R never changes the bits.
+int mfma_rows(int T, int K, int N, int mat) {
+    if (T < 8 || K > 4096) return 1;
+    int best = 1;
+    for (int R = 2; R <= (mat == 2 ? 2 : 4); R *= 2) {
+        const int wgs = (N + 16 * R - 1) / (16 * R);
+        if (wgs >= 256 && wgs * (K / 512) >= 512 * R) best = R;
+    }
+    return best;
+}
+
 template <int MAT>
 hipError_t launch_mfma(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
-    const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)G);
-    switch (a.K) {
-        case 1024: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<2, 1, MAT>), grid, dim3(128), 0, stream, a, sw); break;
-        case 2048: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<4, 1, MAT>), grid, dim3(256), 0, stream, a, sw); break;
-        case 4096: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 1, MAT>), grid, dim3(512), 0, stream, a, sw); break;
-        default:
-            if constexpr (MAT == 1)
-                hipLaunchKernelGGL((fp8_gemv_mfma_kernel<16, 1, 1>), grid, dim3(1024), 0, stream, a, sw);
-            else
-                hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 2, 2>), grid, dim3(512), 0, stream, a, sw);
-            break;
+    const int R = mfma_rows(a.T, a.K, a.N, MAT);
+    if constexpr (MAT == 1) {
+        if (R == 4) launch_mfma_r<1, 4>(a, sw, G, stream);
+        else if (R == 2) launch_mfma_r<1, 2>(a, sw, G, stream);
+        else launch_mfma_r<1, 1>(a, sw, G, stream);
+    } else {
+        if (R == 2) launch_mfma_r<2, 2>(a, sw, G, stream);
+        else launch_mfma_r<2, 1>(a, sw, G, stream);
     }
     return hipGetLastError();
 }
@@ -821,7 +878,7 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
 int launch(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
     if (tile_ok(a)) {
-        e = use_mfma(a.T, a.K, a.N) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
+        e = use_mfma(a.T, a.K, a.N, a.xstride) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
                                      : launch_tile<1>(a, SwigluArgs{}, G, stream);
     } else {
         const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);
@@ -920,7 +977,7 @@ extern "C" int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, i
     ma.n_mats = n_mats;
     bool tile = true;
     bool mfma = true;
-    for (int m = 0; m < n_mats; ++m) mfma = mfma && use_mfma(T, K, N[m]);
+    for (int m = 0; m < n_mats; ++m) mfma = mfma && use_mfma(T, K, N[m], x_row_stride);
     int blocks = 0;
     for (int m = 0; m < n_mats; ++m) {
         Fp8Args a = ma.base;
@@ -988,7 +1045,7 @@ extern "C" int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, 
         return -6;
     }
     const SwigluArgs sw{W3_fp8, W3_scale, limit, clamp_up};
-    if (use_mfma(T, K, N)) {
+    if (use_mfma(T, K, N, x_row_stride)) {
         const hipError_t e = launch_mfma<2>(a, sw, 1, stream);
         if (e != hipSuccess) {
             std::fprintf(stderr, "fp8_e4m3_swiglu_gemv launch failed: %s\n", hipGetErrorString(e));
@@ -1056,7 +1113,7 @@ extern "C" int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* re
                       eps, reinterpret_cast<uint16_t*>(x_norm), reinterpret_cast<uint16_t*>(new_residual)};
     const int KC = K / 16;
     hipError_t e;
-    if (!use_mfma(T, K, N)) {
+    if (!use_mfma(T, K, N, K)) {
         // One launch: the norm, then the GEMV slice of each workgroup.
         const dim3 grid((unsigned)((N + 4 * 256 / KC - 1) / (4 * 256 / KC)));
 #define DSV4_NG(TTV, RES)                                                                                          \
