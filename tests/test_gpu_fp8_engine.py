@@ -83,14 +83,14 @@ def test_fp8_matrix_core_path(device, N, K, T):
 
 
 @pytest.mark.parametrize("N,K,T", [(8192, 4096, 8), (16384, 4096, 9), (16400, 1024, 16), (8192, 2048, 13),
-                                   (8200, 2048, 8)])
+                                   (8200, 2048, 8), (16400, 4096, 12)])
 def test_fp8_matrix_core_row_blocks(device, N, K, T):
     """Large N at T >= 8 runs 2 or 4 16-row blocks per wave on one set of
     activation registers (R = 2: 8192 x 4096, 16400 x 1024, 8192 x 2048,
-    8200 x 2048; R = 4: 16384 x 4096; a ragged N leaves the last workgroup's
-    blocks partly past the matrix): against the oracle, and the first four
-    tokens equal a T = 4 call (one block per wave) bit for bit, since the
-    blocking does not change a row's sums."""
+    8200 x 2048; R = 4: 16384 x 4096, 16400 x 4096; a ragged N leaves the
+    last workgroup's blocks partly past the matrix): against the oracle, and
+    the first four tokens equal a T = 4 call (one block per wave) bit for bit,
+    since the blocking does not change a row's sums."""
     announce(f"fp8_e4m3_gemv matrix-core row blocks N={N} K={K} T={T}")
     w, s = synth.fp8_weight(16800 + N + K, N, K)
     x = synth.normal_bf16(16900 + T + K, (T, K))
@@ -101,18 +101,24 @@ def test_fp8_matrix_core_row_blocks(device, N, K, T):
     assert np.array_equal(four, got[:4])
 
 
-def test_fp8_matrix_core_row_blocks_grouped(device):
-    """Two groups of 8192 rows at T = 8 (two blocks per wave in each group):
-    each group has the bits of a single GEMV on its slice."""
-    G, N, K, T = 2, 8192, 2048, 8
+@pytest.mark.parametrize("N", [8192, 8200])
+def test_fp8_matrix_core_row_blocks_grouped(device, N):
+    """Two groups at T = 8 with two 16-row blocks per wave in each group; with
+    8200 rows the second group starts 8 rows into a scale tile and both end
+    inside a workgroup. Against the oracle; a group that starts on a scale
+    tile has the bits of a single GEMV on its slice."""
+    G, K, T = 2, 2048, 8
     announce(f"fp8_e4m3_gemv_grouped matrix-core row blocks G={G} N={N} K={K} T={T}")
-    w, s = synth.fp8_weight(17000, G * N, K)
+    w, s = synth.fp8_weight(17000 + N, G * N, K)
     x = synth.normal_bf16(17001, (T, G, K))
     tw, ts, xd = dev_u8(w, device), dev_u8(s, device), dev_bf16(x, device)
     got = host_bits(fp8b.fp8_e4m3_gemv_grouped(tw, ts, xd, G)).reshape(T, G, N)
     assert_close(got.reshape(T, -1), mx.fp8_gemv_grouped(x, w, s, G).reshape(T, -1), "grouped row blocks")
     for g in range(G):
-        yg = fp8b.fp8_e4m3_gemv(tw[g * N:(g + 1) * N], ts[g * N // 128:(g + 1) * N // 128], xd[:, g].contiguous())
+        if (g * N) % 128:
+            continue
+        r0 = g * N // 128
+        yg = fp8b.fp8_e4m3_gemv(tw[g * N:(g + 1) * N], ts[r0:r0 + (N + 127) // 128], xd[:, g].contiguous())
         assert np.array_equal(host_bits(yg).reshape(T, N), got[:, g])
 
 
@@ -134,7 +140,7 @@ def test_fp8_matrix_core_groups_straddle_scale_tiles(device):
 
 
 @pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (2048, 4096, 8), (2048, 8192, 3), (1024, 2048, 12),
-                                   (8192, 2048, 8)])
+                                   (8192, 2048, 8), (8200, 2048, 9)])
 def test_fp8_swiglu_matrix_core(device, N, K, T):
     """The fused SwiGLU on the matrix cores (K = 8192 runs two passes per
     wave; 8192 rows at T = 8 two 16-row blocks per wave): against the oracle,
