@@ -23,7 +23,10 @@ configurations measured in the same run (config 3 at T=4 and T=16, the
 reference's routed dispatch, config 4's 43-layer decode sweep and its 512-token
 prefill chunk), `kernels` the other drop-in kernels at BASELINE.json's shapes
 and the engine's FP8 shapes. `cpu_baseline` times the CPU oracle (dequant +
-fp32 matmul, the reference's CPU path) on one step.
+fp32 matmul, the reference's CPU path) on one step. `read_floor` streams the
+byte counts of stage A, stage B and the whole layer once with a read-only
+kernel: what the HBM delivers for that many bytes in one pass, beside the
+kernels' times (`copy_ceiling_gbs` is torch's 1 GiB copy).
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--layers L]
                     [--no-configs] [--no-kernels] [--no-cpu-baseline]
@@ -581,6 +584,36 @@ def add_traffic(kernels: dict) -> None:
 
 # ----------------------------------------------------------- CPU baseline ---
 
+def read_floor_case(torch, dev, cases: dict) -> dict:
+    """The HBM read floor for the byte counts of the timed launches: a
+    read-only kernel (runtime.fill.read_floor: contiguous chunk per workgroup,
+    16-byte loads, 8 in flight per thread) streams the same number of bytes,
+    rotating over 1 GiB so that they come from HBM; the faster of 1,024 and
+    2,048 workgroups, 200 launches issued back to back by the library and
+    timed by HIP events. cases maps a name to (bytes, the kernel's measured
+    µs)."""
+    from runtime import fill
+    pool = 1 << 30
+    buf = torch.empty(pool + (1 << 28), dtype=torch.uint8, device=dev)
+    fill.fill_uniform_u8(buf, 4242)
+    sink = torch.empty(2048 * 512, dtype=torch.int32, device=dev)
+    tm = Timer(torch)
+    out = {"kernel": "dsv4_read_floor (libdsv4_fill.so)"}
+    for name, (nbytes, kernel_us) in cases.items():
+        nb = int(nbytes) // 16 * 16
+        nrot = max(1, pool // nb)
+        best = float("inf")
+        for wgs in (1024, 2048):
+            fill.read_floor(buf, nb, wgs, sink, nrot, 10)
+            reps = 200
+            ms = tm.ms(lambda: fill.read_floor(buf, nb, wgs, sink, nrot, reps))
+            best = min(best, ms * 1e3 / reps)
+        out[name] = {"bytes": nb, "floor_us": round(best, 3), "floor_gbs": round(gbs(nb, best), 1),
+                     "kernel_us": round(kernel_us, 3), "kernel_over_floor": round(kernel_us / best, 3)}
+    del buf, sink
+    return out
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -838,6 +871,10 @@ def main() -> int:
     copy_ms = Timer(torch).ms(lambda: [dst.copy_(src) for _ in range(5)]) / 5
     result["copy_ceiling_gbs"] = round(2 * src.numel() / (copy_ms * 1e-3) / 1e9, 1)
     del src, dst
+    # the HBM read floor for the same byte counts (one pass of a read-only kernel)
+    result["read_floor"] = read_floor_case(torch, dev, {
+        "stage_A": (a_bytes, a_us), "stage_B": (b_bytes, b_us),
+        "layer_one_pass": (a_bytes + b_bytes, result["moe_layer_us"])})
     print(json.dumps(result), flush=True)
     return 0
 

@@ -35,6 +35,25 @@ def test_device_fill_matches_numpy_generator(device):
     assert np.array_equal(s.cpu().numpy(), synth.uniform_u8(99, 5, 4099, 119, 125))
 
 
+def test_read_floor_streams_without_writing(device):
+    """The read-floor harness kernel (bench.py's `read_floor`): three launches
+    rotating over two ranges of a ragged size (the last workgroup shorter)
+    leave the source untouched and write nothing to the sink for fill data
+    (it stores only when a thread's folded words hit one constant)."""
+    announce("dsv4_read_floor 2 x 1000000 bytes, 3 launches, 1024 workgroups")
+    n = 1_000_000
+    src = torch.empty(2 * n, dtype=torch.uint8, device=device)
+    fill.fill_uniform_u8(src, 4242)
+    before = src.cpu().numpy().copy()
+    sink = torch.zeros(1024 * 512, dtype=torch.int32, device=device)
+    fill.read_floor(src, n, 1024, sink, rotate=2, launches=3)
+    torch.cuda.synchronize()
+    assert np.array_equal(src.cpu().numpy(), before)
+    assert int(torch.count_nonzero(sink)) == 0
+    with pytest.raises(RuntimeError):
+        fill.read_floor(src, n - 8, 1024, sink)        # not a multiple of 16 bytes
+
+
 # ----------------------------------------------------------------- dequant --
 
 def test_mxfp4_dequant_exhaustive_bit_exact(device):
