@@ -361,11 +361,11 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
     const int g = lane >> 4;
     const int n0 = blk * 16 * R;
     // Activations through a buffer bounded at the T token rows: the lanes of
-    // token columns T..15 read zeros without touching memory (their outputs
-    // are dropped), so x costs T rows of loads, not 16.
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)gv.x, (short)0, (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2), 0x00020000);
-    const int xoff = (int)(((int64_t)r * a.xstride + 16 * g) * 2);
+    // token columns T..15 start at the bound and read zeros without touching
+    // memory (their outputs are dropped), so x costs T rows of loads, not 16.
+    const int xbytes = (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2);   // < 2^31 (use_mfma)
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)gv.x, (short)0, xbytes, 0x00020000);
+    const uint32_t xoff = r < a.T ? (uint32_t)(((int64_t)r * a.xstride + 16 * g) * 2) : (uint32_t)xbytes;
     const uint8_t* wr[MAT][R];
     const uint8_t* sr[MAT][R];
 #pragma unroll
@@ -400,8 +400,8 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
         u32x4 wv[MAT][R][L];
 #pragma unroll
         for (int j = 0; j < L; ++j) {
-            xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + (k0 + 64 * j) * 2, 0, 0);
-            xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff + (k0 + 64 * j) * 2 + 16, 0, 0);
+            xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u), 0, 0);
+            xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u + 16u), 0, 0);
 #pragma unroll
             for (int b = 0; b < R; ++b)
 #pragma unroll
