@@ -594,14 +594,15 @@ def read_floor_case(torch, dev, cases: dict) -> dict:
     µs)."""
     from runtime import fill
     pool = 1 << 30
-    buf = torch.empty(pool + (1 << 28), dtype=torch.uint8, device=dev)
+    largest = max(int(nbytes) // 16 * 16 for nbytes, _ in cases.values())
+    buf = torch.empty(max(pool, largest), dtype=torch.uint8, device=dev)
     fill.fill_uniform_u8(buf, 4242)
     sink = torch.empty(2048 * 512, dtype=torch.int32, device=dev)
     tm = Timer(torch)
     out = {"kernel": "dsv4_read_floor (libdsv4_fill.so)"}
     for name, (nbytes, kernel_us) in cases.items():
         nb = int(nbytes) // 16 * 16
-        nrot = max(1, pool // nb)
+        nrot = max(1, pool // nb)          # ranges past 1 GiB are read from one place (beyond the MALL anyway)
         best = float("inf")
         for wgs in (1024, 2048):
             fill.read_floor(buf, nb, wgs, sink, nrot, 10)
