@@ -26,7 +26,8 @@ and the engine's FP8 shapes. `cpu_baseline` times the CPU oracle (dequant +
 fp32 matmul, the reference's CPU path) on one step. `read_floor` streams the
 byte counts of stage A, stage B and the whole layer once with a read-only
 kernel: what the HBM delivers for that many bytes in one pass, beside the
-kernels' times (`copy_ceiling_gbs` is torch's 1 GiB copy).
+kernels' times (`copy_ceiling_gbs` is torch's 1 GiB copy); the prefill entry
+of `configs` has the same for its weight bytes.
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--layers L]
                     [--no-configs] [--no-kernels] [--no-cpu-baseline]
@@ -809,6 +810,11 @@ def main() -> int:
         c4 = config4_case(torch, dev, 8, 2, args.c4_layers)
         configs["cfg4_decode"] = c4["decode"]
         configs["cfg4_prefill"] = c4["prefill"]
+        del c4
+        torch.cuda.empty_cache()
+        pf = configs["cfg4_prefill"]
+        pf["read_floor"] = read_floor_case(torch, dev, {
+            "layer_bytes": (pf["algorithmic_bytes_per_layer"], pf["us_per_layer"])})
 
     kernels = None
     if not args.no_kernels:
