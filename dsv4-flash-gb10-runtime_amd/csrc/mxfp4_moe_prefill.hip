@@ -12,7 +12,8 @@
 //
 // Launches (one stream, caller's workspace, no allocation, no atomics on
 // results):
-//   1. routing: pairs (token, k) grouped by expert, 64-token tiles per expert;
+//   1. routing: pairs (token, k) grouped by expert, 64-token tiles per expert
+//      (listed longest first);
 //   2. stage A: per (tile, 64 hidden rows) M[pair, h] = bf16(silu(g) * u);
 //   3. stage B: per (tile, 64 output rows) Y[pair, o] = w * (W2_e . M[pair]) in fp32;
 //   4. combine: out[t, o] = bf16( sum_k Y[pos(t, k), o] ), k in order.
@@ -81,19 +82,25 @@ __device__ __forceinline__ int block_scan(int v, int* wtot) {
 }
 
 // One workgroup: count the pairs of each expert (LDS atomics give each pair a
-// slot inside its expert), scan counts and tile counts, then write the pair
-// lists, the (t, k) -> pair map and the tile list. Pair order inside an
-// expert may vary between runs; results do not depend on it.
+// slot inside its expert), scan the counts, then write the pair lists, the
+// (t, k) -> pair map and the tile list: every full 64-pair tile first, then
+// the partial tiles by decreasing size, so that the longest tiles are
+// dispatched first and the grid does not end on a few long ones (2% of the
+// layer against tiles in expert order). Pair order inside an expert and the
+// order of tiles of one size may vary between runs; results depend on
+// neither.
 __global__ __launch_bounds__(kRouteThreads) void prefill_route_kernel(const int32_t* ids,
                                                                       const float* w, int P,
                                                                       int topk, int n_experts,
                                                                       PrefillTables pt) {
     __shared__ int cnt[kMaxExperts];
     __shared__ int off[kMaxExperts];
-    __shared__ int toff[kMaxExperts];
     __shared__ int wtot[kRouteThreads / 64];
+    __shared__ int hcur[kTileTok];          // next position of a partial tile of each size
+    __shared__ int nfull;
     const int tid = threadIdx.x;
     for (int e = tid; e < kMaxExperts; e += kRouteThreads) cnt[e] = 0;
+    if (tid < kTileTok) hcur[tid] = 0;
     __syncthreads();
     for (int i = tid; i < P; i += kRouteThreads) {
         const int e = ids[i];
@@ -101,16 +108,30 @@ __global__ __launch_bounds__(kRouteThreads) void prefill_route_kernel(const int3
     }
     __syncthreads();
     const int c = tid < n_experts ? cnt[tid] : 0;
-    const int nt = (c + kTileTok - 1) / kTileTok;
+    const int nf = c / kTileTok;                 // full tiles
+    const int rem = c % kTileTok;                // size of the partial tile (0: none)
     const int ci = block_scan(c, wtot);
-    const int ti = block_scan(nt, wtot);
-    if (tid < n_experts) {
-        off[tid] = ci - c;
-        toff[tid] = ti - nt;
-    }
+    const int fi = block_scan(nf, wtot);
+    if (rem > 0) atomicAdd(&hcur[rem], 1);
+    if (tid < n_experts) off[tid] = ci - c;
     if (tid == kRouteThreads - 1) {
-        pt.header[0] = ti;
+        nfull = fi;
         pt.header[1] = ci;
+    }
+    __syncthreads();
+    // Tile list: full tiles first, then partial tiles by decreasing size, so
+    // the longest tiles are dispatched first (the order does not change any
+    // result). Wave 0 turns the size histogram into start positions.
+    if (tid < 64) {
+        const int s = 63 - tid;                  // lane l: size 63 - l (lane 63: size 0, none)
+        const int h = s > 0 ? hcur[s] : 0;
+        int incl = h;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int up = __shfl_up(incl, d, 64);
+            if (tid >= d) incl += up;
+        }
+        if (s > 0) hcur[s] = nfull + incl - h;
+        if (tid == 63) pt.header[0] = nfull + incl;
     }
     __syncthreads();
     for (int i = tid; i < P; i += kRouteThreads) {
@@ -124,11 +145,17 @@ __global__ __launch_bounds__(kRouteThreads) void prefill_route_kernel(const int3
         }
     }
     if (tid < n_experts) {
-        for (int j = 0; j < nt; ++j) {
-            const int t = toff[tid] + j;
+        for (int j = 0; j < nf; ++j) {
+            const int t = fi - nf + j;
             pt.tile_e[t] = tid;
             pt.tile_p0[t] = off[tid] + kTileTok * j;
-            pt.tile_n[t] = min(kTileTok, c - kTileTok * j);
+            pt.tile_n[t] = kTileTok;
+        }
+        if (rem > 0) {
+            const int t = atomicAdd(&hcur[rem], 1);
+            pt.tile_e[t] = tid;
+            pt.tile_p0[t] = off[tid] + kTileTok * nf;
+            pt.tile_n[t] = rem;
         }
     }
 }
