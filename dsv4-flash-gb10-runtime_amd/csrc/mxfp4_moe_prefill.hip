@@ -51,6 +51,7 @@ constexpr int kMaxTopk = 16;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxRed = 8192;
 constexpr int kRouteThreads = 1024;
+constexpr int kRouteRegs = 8;        // routing entries per thread held in registers
 
 struct PrefillTables {
     int32_t* header;     // [0] tiles, [1] routed pairs
@@ -99,12 +100,36 @@ __global__ __launch_bounds__(kRouteThreads) void prefill_route_kernel(const int3
     __shared__ int hcur[kTileTok];          // next position of a partial tile of each size
     __shared__ int nfull;
     const int tid = threadIdx.x;
+    // Up to kRouteRegs * kRouteThreads entries, each thread keeps its
+    // entries' ids, weights and slots in registers, with every load issued
+    // at once; larger chunks go through pos[] in memory (a round trip per
+    // entry and pass).
+    const bool regs = P <= kRouteRegs * kRouteThreads;
+    int e_r[kRouteRegs], s_r[kRouteRegs];
+    float w_r[kRouteRegs];
+    if (regs) {
+#pragma unroll
+        for (int q = 0; q < kRouteRegs; ++q) {
+            const int i = min(tid + q * kRouteThreads, P - 1);
+            e_r[q] = ids[i];
+            w_r[q] = w[i];
+        }
+    }
     for (int e = tid; e < kMaxExperts; e += kRouteThreads) cnt[e] = 0;
     if (tid < kTileTok) hcur[tid] = 0;
     __syncthreads();
-    for (int i = tid; i < P; i += kRouteThreads) {
-        const int e = ids[i];
-        pt.pos[i] = (e >= 0 && e < n_experts) ? atomicAdd(&cnt[e], 1) : -1;  // slot inside e
+    if (regs) {
+#pragma unroll
+        for (int q = 0; q < kRouteRegs; ++q) {
+            const int i = tid + q * kRouteThreads;
+            const int e = e_r[q];
+            s_r[q] = (i < P && e >= 0 && e < n_experts) ? atomicAdd(&cnt[e], 1) : -1;  // slot inside e
+        }
+    } else {
+        for (int i = tid; i < P; i += kRouteThreads) {
+            const int e = ids[i];
+            pt.pos[i] = (e >= 0 && e < n_experts) ? atomicAdd(&cnt[e], 1) : -1;
+        }
     }
     __syncthreads();
     const int c = tid < n_experts ? cnt[tid] : 0;
@@ -134,14 +159,30 @@ __global__ __launch_bounds__(kRouteThreads) void prefill_route_kernel(const int3
         if (tid == 63) pt.header[0] = nfull + incl;
     }
     __syncthreads();
-    for (int i = tid; i < P; i += kRouteThreads) {
-        const int e = ids[i];
-        const int slot = pt.pos[i];
-        if (slot >= 0) {
-            const int p = off[e] + slot;
-            pt.pair_tok[p] = i / topk;
-            pt.pair_w[p] = w[i];
-            pt.pos[i] = p;
+    if (regs) {
+#pragma unroll
+        for (int q = 0; q < kRouteRegs; ++q) {
+            const int i = tid + q * kRouteThreads;
+            if (i < P) {
+                int p = -1;
+                if (s_r[q] >= 0) {
+                    p = off[e_r[q]] + s_r[q];
+                    pt.pair_tok[p] = i / topk;
+                    pt.pair_w[p] = w_r[q];
+                }
+                pt.pos[i] = p;
+            }
+        }
+    } else {
+        for (int i = tid; i < P; i += kRouteThreads) {
+            const int e = ids[i];
+            const int slot = pt.pos[i];
+            if (slot >= 0) {
+                const int p = off[e] + slot;
+                pt.pair_tok[p] = i / topk;
+                pt.pair_w[p] = w[i];
+                pt.pos[i] = p;
+            }
         }
     }
     if (tid < n_experts) {

@@ -565,10 +565,12 @@ def test_moe_indexed_equals_packed_dropin(device):
 
 # ------------------------------------------------------- prefill (MFMA) ---
 
-@pytest.mark.parametrize("T,topk,E", [(100, 4, 16), (7, 8, 8), (130, 2, 64)])
+@pytest.mark.parametrize("T,topk,E", [(100, 4, 16), (7, 8, 8), (130, 2, 64), (1024, 8, 32), (1100, 8, 16)])
 def test_moe_prefill_small_vs_oracle(device, T, topk, E):
     """MFMA prefill path against the oracle at small dims, including a
-    duplicate id in a token and ids outside [0, n_experts)."""
+    duplicate id in a token and ids outside [0, n_experts). The routing keeps
+    up to 8,192 entries in registers (1024 x 8 is the largest such chunk) and
+    goes through memory above that (1100 x 8)."""
     K, H, O = 512, 512, 384
     announce(f"mxfp4_moe_prefill T={T} topk={topk} E={E} K={K} H={H} O={O}")
     W1p, W1s = synth.mxfp4_weight(8400 + E, H, K, E)
