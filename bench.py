@@ -548,6 +548,14 @@ def dense_kernels(torch, dev, cpu: bool, counters: bool = False) -> dict:
                                                              cpu_us(lambda: mx.rmsnorm_residual(h, r, g)))
         del Hc, Rc
     add_traffic(out)
+    if not counters:
+        # the read floor for each line's bytes, timed the same way (graph replay)
+        rf = read_floor_case(torch, dev, {k: (e["algorithmic_bytes"], e["us"]) for k, e in out.items()
+                                          if e["algorithmic_bytes"] >= 16}, graph=True)
+        for k, e in out.items():
+            if k in rf:
+                e["read_floor_us"] = rf[k]["floor_us"]
+                e["kernel_over_floor"] = rf[k]["kernel_over_floor"]
     return out
 
 
@@ -585,14 +593,16 @@ def add_traffic(kernels: dict) -> None:
 
 # ----------------------------------------------------------- CPU baseline ---
 
-def read_floor_case(torch, dev, cases: dict) -> dict:
+def read_floor_case(torch, dev, cases: dict, graph: bool = False) -> dict:
     """The HBM read floor for the byte counts of the timed launches: a
     read-only kernel (runtime.fill.read_floor: contiguous chunk per workgroup,
     16-byte loads, 8 in flight per thread) streams the same number of bytes,
-    rotating over 1 GiB so that they come from HBM; the faster of 1,024 and
-    2,048 workgroups, 200 launches issued back to back by the library and
-    timed by HIP events. cases maps a name to (bytes, the kernel's measured
-    µs)."""
+    rotating over 1 GiB so that they come from HBM; the fastest of five
+    launch shapes (256 to 2,048 workgroups of 256 or 512 threads), 200
+    launches issued back to back by the library and
+    timed by HIP events (graph=True: captured in a HIP graph and replayed, as
+    the dense-kernel lines are timed). cases maps a name to (bytes, the
+    kernel's measured µs)."""
     from runtime import fill
     pool = 1 << 30
     largest = max(int(nbytes) // 16 * 16 for nbytes, _ in cases.values())
@@ -605,11 +615,14 @@ def read_floor_case(torch, dev, cases: dict) -> dict:
         nb = int(nbytes) // 16 * 16
         nrot = max(1, pool // nb)          # ranges past 1 GiB are read from one place (beyond the MALL anyway)
         best = float("inf")
-        for wgs in (1024, 2048):
-            fill.read_floor(buf, nb, wgs, sink, nrot, 10)
+        for wgs, thr in ((256, 256), (512, 256), (1024, 256), (1024, 512), (2048, 512)):
+            fill.read_floor(buf, nb, wgs, sink, nrot, 10, thr)
             reps = 200
-            ms = tm.ms(lambda: fill.read_floor(buf, nb, wgs, sink, nrot, reps))
-            best = min(best, ms * 1e3 / reps)
+            if graph:
+                us = tm.graph_us_per_call(lambda: fill.read_floor(buf, nb, wgs, sink, nrot, reps, thr), reps, reps=4)
+            else:
+                us = tm.ms(lambda: fill.read_floor(buf, nb, wgs, sink, nrot, reps, thr)) * 1e3 / reps
+            best = min(best, us)
         out[name] = {"bytes": nb, "floor_us": round(best, 3), "floor_gbs": round(gbs(nb, best), 1),
                      "kernel_us": round(kernel_us, 3), "kernel_over_floor": round(kernel_us / best, 3)}
     del buf, sink

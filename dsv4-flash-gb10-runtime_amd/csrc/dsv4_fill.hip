@@ -82,15 +82,15 @@ __global__ __launch_bounds__(512) void read_floor_kernel(const uint32_t* __restr
 
 // `launches` back-to-back launches on `stream`, launch i streaming the
 // `bytes` at src + (i % rotate) * bytes once with `workgroups` workgroups of
-// 512 threads (src holds rotate * bytes; 16-byte aligned, bytes a multiple of
-// 16). The loop is here so that the host issues launches as fast as the
-// runtime takes them. sink must hold workgroups * 512 words and is written
-// only in the case described at read_floor_kernel. Returns 0, -1 for a bad
-// argument, or a hipError_t from a launch.
+// `threads` (256 or 512) threads (src holds rotate * bytes; 16-byte aligned,
+// bytes a multiple of 16). The loop is here so that the host issues launches
+// as fast as the runtime takes them. sink must hold workgroups * threads
+// words and is written only in the case described at read_floor_kernel.
+// Returns 0, -1 for a bad argument, or a hipError_t from a launch.
 extern "C" int dsv4_read_floor(const void* src, uint64_t bytes, int rotate, int launches, int workgroups,
-                               uint32_t* sink, hipStream_t stream) {
+                               int threads, uint32_t* sink, hipStream_t stream) {
     if (!src || !sink || bytes == 0 || bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0 ||
-        rotate < 1 || launches < 1 || workgroups < 1 || workgroups > 65535)
+        rotate < 1 || launches < 1 || workgroups < 1 || workgroups > 65535 || (threads != 256 && threads != 512))
         return -1;
     const uint64_t n16 = bytes / 16;
     const uint64_t per = (n16 + (uint64_t)workgroups - 1) / (uint64_t)workgroups;
@@ -98,7 +98,7 @@ extern "C" int dsv4_read_floor(const void* src, uint64_t bytes, int rotate, int 
     for (int i = 0; i < launches; ++i) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(src) +
                                                               (uint64_t)(i % rotate) * bytes);
-        hipLaunchKernelGGL(read_floor_kernel, dim3(wgs), dim3(512), 0, stream, p, n16, per, sink);
+        hipLaunchKernelGGL(read_floor_kernel, dim3(wgs), dim3((unsigned)threads), 0, stream, p, n16, per, sink);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return (int)e;
     }

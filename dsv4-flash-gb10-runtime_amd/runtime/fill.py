@@ -27,7 +27,7 @@ def _load_lib() -> ctypes.CDLL:
                                              ctypes.c_void_p]
         lib.dsv4_fill_uniform_u8.restype = ctypes.c_int
         lib.dsv4_read_floor.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
-                                        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         lib.dsv4_read_floor.restype = ctypes.c_int
         _LIB = lib
     return _LIB
@@ -44,16 +44,17 @@ def fill_uniform_u8(t: torch.Tensor, seed: int, offset: int = 0, lo: int = 0, hi
 
 
 def read_floor(src: torch.Tensor, nbytes: int, workgroups: int, sink: torch.Tensor,
-               rotate: int = 1, launches: int = 1) -> None:
+               rotate: int = 1, launches: int = 1, threads: int = 512) -> None:
     """`launches` back-to-back launches of the read-only kernel, launch i
     streaming the `nbytes` at byte (i % rotate) * nbytes of the GPU tensor
-    `src` once (the HBM read floor for that many bytes); sink is an int32 GPU
-    tensor of at least workgroups * 512 elements."""
+    `src` once with `workgroups` workgroups of `threads` (256 or 512) threads
+    (the HBM read floor for that many bytes); sink is an int32 GPU tensor of
+    at least workgroups * threads elements."""
     if not src.is_cuda or not src.is_contiguous() or rotate * nbytes > src.numel() * src.element_size():
         raise ValueError("read_floor needs a contiguous GPU tensor holding rotate * nbytes bytes")
-    if not sink.is_cuda or sink.dtype != torch.int32 or sink.numel() < workgroups * 512:
-        raise ValueError("read_floor needs an int32 GPU sink of workgroups * 512 elements")
-    rc = _load_lib().dsv4_read_floor(_lib.vp(src), nbytes, rotate, launches, workgroups, _lib.vp(sink),
+    if not sink.is_cuda or sink.dtype != torch.int32 or sink.numel() < workgroups * threads:
+        raise ValueError("read_floor needs an int32 GPU sink of workgroups * threads elements")
+    rc = _load_lib().dsv4_read_floor(_lib.vp(src), nbytes, rotate, launches, workgroups, threads, _lib.vp(sink),
                                      ctypes.c_void_p(_lib.stream_ptr(src.device)))
     if rc != 0:
         raise RuntimeError(f"dsv4_read_floor returned {rc}")

@@ -47,6 +47,7 @@ def test_read_floor_streams_without_writing(device):
     before = src.cpu().numpy().copy()
     sink = torch.zeros(1024 * 512, dtype=torch.int32, device=device)
     fill.read_floor(src, n, 1024, sink, rotate=2, launches=3)
+    fill.read_floor(src, n, 300, sink, rotate=2, launches=2, threads=256)
     torch.cuda.synchronize()
     assert np.array_equal(src.cpu().numpy(), before)
     assert int(torch.count_nonzero(sink)) == 0
