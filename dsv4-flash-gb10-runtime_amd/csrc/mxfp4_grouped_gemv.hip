@@ -1506,7 +1506,19 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
     }
     if (lane == 63) scan[wave] = incl;
     __syncthreads();
-    for (int w = 0; w < wave; ++w) incl += scan[w];
+    // The wave totals in wave order: lanes 0..15 of every wave hold them and
+    // one shuffle scan gives this wave's offset and the grand total (no
+    // serial pass over LDS).
+    constexpr int kRouteWaves = kRouteThreads / 64;
+    const int wt = lane < kRouteWaves ? scan[lane] : 0;
+    int wincl = wt;
+#pragma unroll
+    for (int d = 1; d < kRouteWaves; d <<= 1) {
+        const int up = __shfl_up(wincl, d, 64);
+        if (lane >= d) wincl += up;
+    }
+    const int total = __shfl(wincl, kRouteWaves - 1, 64);
+    incl += wave > 0 ? __shfl(wincl, wave - 1, 64) : 0;
     int run = incl - local;
 #pragma unroll
     for (int q = 0; q < kExpPerThread; ++q) {
@@ -1528,8 +1540,6 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* l
     {
         // Slots past the routed ones get a valid expert id, so the one-token
         // kernels may form weight addresses from any slot before checking it.
-        int total = 0;
-        for (int w = 0; w < kRouteThreads / 64; ++w) total += scan[w];
         for (int u = (total >> 16) + tid; u < rt.n_slots; u += kRouteThreads) rt.uexp[u] = 0;
     }
     __syncthreads();
