@@ -76,8 +76,16 @@ __device__ __forceinline__ int block_scan(int v, int* wtot) {
     }
     if (lane == 63) wtot[wave] = v;
     __syncthreads();
-    int add = 0;
-    for (int w = 0; w < wave; ++w) add += wtot[w];
+    // The 16 wave totals in wave order: one shuffle scan over lanes 0..15.
+    constexpr int kWavesR = kRouteThreads / 64;
+    const int wt = lane < kWavesR ? wtot[lane] : 0;
+    int wincl = wt;
+#pragma unroll
+    for (int d = 1; d < kWavesR; d <<= 1) {
+        const int up = __shfl_up(wincl, d, 64);
+        if (lane >= d) wincl += up;
+    }
+    const int add = wave > 0 ? __shfl(wincl, wave - 1, 64) : 0;
     __syncthreads();
     return v + add;
 }
