@@ -129,6 +129,37 @@ def test_grouped_dropin_many_experts(device, n_exp, K, H, O):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_hidden_at_cap(device, T):
+    """hidden = 4096, the grouped path's cap: stage B with two MX blocks per
+    lane (the one-token kernel at T = 1, the general kernel at T = 4), through
+    the expert-indexed entry and the gated layer, and the drop-in with 8
+    experts, against the oracle."""
+    E, K, H, O, k = 16, 2048, 4096, 512, 8
+    announce(f"mxfp4 hidden 4096 T={T} E={E} K={K} O={O}")
+    w = moe.make_moe_weights(12600 + T, E, K, H, O, device)
+    x = synth.normal_bf16(12610 + T, (T, K))
+    logits = synth.gating_logits(12620 + T, T, E)
+    ids, wt = mx.route_sigmoid_topk(logits, k)
+    xd = dev_bf16(x, device)
+    fn = _host_expert_fn(w)
+    ref = mx.moe_layer(x, fn, ids, wt, O, n_experts=E)
+    idp = host_bits(gb.mxfp4_moe_grouped_gemv(xd, w.W1, w.W3, w.W2, torch.from_numpy(ids).to(device),
+                                              dev_f32(wt, device)))
+    assert_close(idp, ref, f"hidden 4096 ids path T={T}")
+    gated = host_bits(gb.mxfp4_moe_layer(xd, dev_f32(logits, device), w.W1, w.W3, w.W2, k))
+    assert_close(gated, ref, f"hidden 4096 gated layer T={T}")
+    if T == 1:
+        sub = {m: {"packed": getattr(w, m)["packed"][:8], "scale": getattr(w, m)["scale"][:8]}
+               for m in ("W1", "W3", "W2")}
+        r = np.linspace(0.05, 0.2, 8).astype(np.float32)
+        out = host_bits(gb.mxfp4_grouped_gemv(sub["W1"], sub["W3"], sub["W2"], None, xd[0], dev_f32(r, device)))
+        ref8 = mx.moe_layer(x, fn, np.arange(8, dtype=np.int32)[None, :], r[None, :], O)
+        assert_close(out, ref8[0], "hidden 4096 drop-in n_exp=8")
+    del w
+    torch.cuda.empty_cache()
+
+
 def test_moe_layer_top16_one_token(device):
     """One token, top-16 of 64 experts at hidden 2048: 16 routed slots, the
     general one-token stage B, through the gated and the ids paths."""
