@@ -166,6 +166,28 @@ def test_fp8_gemv_tile_path_tokens_and_ragged_n(device, N, K, T):
     assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 tile N={N} K={K} T={T}")
 
 
+@pytest.mark.parametrize("N,K,T,odd_stride", [(77, 384, 1, False), (77, 384, 3, False), (130, 3200, 2, False),
+                                              (64, 12288, 1, False), (50, 12288, 3, False),
+                                              (33, 16384, 2, False), (140, 4096, 1, True),
+                                              (45, 4096, 5, True), (20, 12288, 2, True)])
+def test_fp8_gemv_general_path(device, N, K, T, odd_stride):
+    """K off the tile set (a multiple of 128 up to the 16384 cap; rows longer
+    than 4096 are walked in segments, once per token) and weight rows at an odd
+    byte stride (unaligned 16-byte loads): the general kernel, against the oracle."""
+    announce(f"fp8_e4m3_gemv general N={N} K={K} T={T} odd_stride={odd_stride}")
+    w, s = synth.fp8_weight(4500 + N + K + T, N, K)
+    x = synth.normal_bf16(4600 + T, (T, K))
+    if odd_stride:
+        buf = torch.zeros(N, K + 1, dtype=torch.uint8, device=device)
+        buf[:, :K] = dev_u8(w, device)
+        tw = buf[:, :K]
+    else:
+        tw = dev_u8(w, device)
+    xd = dev_bf16(x, device)
+    y = fp8b.fp8_e4m3_gemv(tw, dev_u8(s, device), xd if T > 1 else xd[0])
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 general N={N} K={K} T={T}")
+
+
 def test_fp8_gemv_long_rows_and_ragged_n(device):
     N, K, T = 200, 8192, 3
     announce(f"fp8_e4m3_gemv N={N} K={K} T={T} (K = 8192 on the tile path)")
