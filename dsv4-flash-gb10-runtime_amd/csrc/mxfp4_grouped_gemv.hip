@@ -33,6 +33,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 
 #include "dsv4_device.h"
@@ -1769,6 +1770,20 @@ struct MoeCall {
     ExpertSet es;
 };
 
+// The extensions reject a null required pointer before any launch; the
+// drop-in mxfp4_grouped_gemv_topk keeps the reference's checks (shapes only).
+constexpr int kNullOperand = -10;
+
+bool operands_set(const char* who, std::initializer_list<const void*> ps) {
+    for (const void* p : ps) {
+        if (p == nullptr) {
+            std::fprintf(stderr, "%s: a required pointer is null\n", who);
+            return false;
+        }
+    }
+    return true;
+}
+
 int moe_validate(int T, int topk, int n_experts, int K_in, int hidden, int out_dim) {
     if (K_in % kBlkElems != 0 || K_in < kBlkElems) return -1;
     if (hidden % kBlkElems != 0 || hidden < kBlkElems) return -2;
@@ -2058,6 +2073,7 @@ int route_topk(const float* logits, int T, int n_experts, int topk, Scoring sc, 
                      topk, sc.mode);
         return -1;
     }
+    if (!operands_set("mxfp4 route", {logits, ids, weights})) return kNullOperand;
     hipLaunchKernelGGL(moe_route_topk_kernel, dim3((unsigned)T), dim3(64), 0, stream, logits, n_experts,
                        topk, sc, ids, weights);
     const hipError_t e = hipGetLastError();
@@ -2097,6 +2113,7 @@ extern "C" int mxfp4_moe_build_routing(const int32_t* ids, const float* weights,
                                        hipStream_t stream) {
     const int v = moe_validate(T, topk, n_experts, kBlkElems, hidden, 1);
     if (v != 0) return v;
+    if (!operands_set("mxfp4_moe_build_routing", {ids, weights, workspace})) return kNullOperand;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     return launch_route(nullptr, ids, weights, T, topk, n_experts, nullptr, nullptr, c, stream);
 }
@@ -2107,6 +2124,8 @@ extern "C" int mxfp4_moe_swiglu(const dsv4_bf16_t* x, const uint8_t* W1_packed,
                                 int hidden, void* workspace, hipStream_t stream) {
     const int v = moe_validate(T, topk, n_experts, K_in, hidden, 1);
     if (v != 0) return v;
+    if (!operands_set("mxfp4_moe_swiglu", {x, W1_packed, W3_packed, W1_scale, W3_scale, workspace}))
+        return kNullOperand;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     return launch_swiglu(x, W1_packed, W3_packed, W1_scale, W3_scale, K_in, hidden, T, c, stream);
 }
@@ -2118,6 +2137,8 @@ extern "C" int mxfp4_moe_gate_swiglu(const dsv4_bf16_t* x, const float* logits, 
     const int v = moe_validate(T, topk, n_experts, K_in, hidden, 1);
     if (v != 0) return v;
     if (topk > n_experts) return -4;
+    if (!operands_set("mxfp4_moe_gate_swiglu", {x, logits, W1_packed, W3_packed, W1_scale, W3_scale, workspace}))
+        return kNullOperand;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     return moe_gate_swiglu_impl(x, logits, W1_packed, W3_packed, W1_scale, W3_scale, T, topk, n_experts, K_in,
                                 hidden, ids_out, weights_out, c, Scoring{kScoreSigmoid, 1.0f}, stream);
@@ -2128,6 +2149,7 @@ extern "C" int mxfp4_moe_down(const uint8_t* W2_packed, const uint8_t* W2_scale,
                               void* workspace, hipStream_t stream) {
     const int v = moe_validate(T, topk, n_experts, kBlkElems, hidden, out_dim);
     if (v != 0) return v;
+    if (!operands_set("mxfp4_moe_down", {W2_packed, W2_scale, out, workspace})) return kNullOperand;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     return launch_down(W2_packed, W2_scale, T, hidden, out_dim, out, c, stream);
 }
@@ -2210,6 +2232,9 @@ extern "C" int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x, const uint8_t* W1_pa
                                       void* workspace, hipStream_t stream) {
     const int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
     if (v != 0) return v;
+    if (!operands_set("mxfp4_moe_grouped_gemv", {x, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale,
+                                                 ids, weights, out, workspace}))
+        return kNullOperand;
     return moe_grouped_impl(x, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale, ids, weights, T,
                             topk, n_experts, K_in, hidden, out_dim, out, workspace, stream);
 }
@@ -2231,6 +2256,9 @@ extern "C" int mxfp4_moe_grouped_gemv_noalloc(const dsv4_bf16_t* x, const uint8_
                      T, topk, hidden, need, kScratchBytes);
         return -8;
     }
+    if (!operands_set("mxfp4_moe_grouped_gemv_noalloc", {x, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale,
+                                                         W2_scale, ids, weights, out}))
+        return kNullOperand;
     void* ws = nullptr;
     const int r = scratch_for_current_device(&ws);
     if (r != 0) return r;
@@ -2248,6 +2276,9 @@ extern "C" int mxfp4_moe_layer(const dsv4_bf16_t* x, const float* logits,
     const int v = moe_validate(T, topk, n_experts, K_in, hidden, out_dim);
     if (v != 0) return v;
     if (topk > n_experts) return -4;
+    if (!operands_set("mxfp4_moe_layer", {x, logits, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale,
+                                          out, workspace}))
+        return kNullOperand;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     return moe_layer_impl(x, logits, W1_packed, W3_packed, W2_packed, W1_scale, W3_scale, W2_scale, T, topk,
                           n_experts, K_in, hidden, out_dim, out, ids_out, weights_out, c,
@@ -2270,10 +2301,9 @@ extern "C" int mxfp4_moe_routed_dispatch(const dsv4_bf16_t* x, const dsv4_bf16_t
     if (v != 0) return v;
     if (topk > n_experts) return -4;
     if (router_validate(T, n_experts, K_in) != 0) return -4;
-    if (!workspace || !out) {
-        std::fprintf(stderr, "mxfp4 dispatch: null workspace or out\n");
-        return -3;
-    }
+    if (!operands_set("mxfp4_moe_routed_dispatch", {x, W_gate, W1_packed, W3_packed, W2_packed, W1_scale,
+                                                    W3_scale, W2_scale, out, workspace}))
+        return kNullOperand;
     const MoeCall c = moe_call(T, topk, n_experts, hidden, workspace);
     uint8_t* base = reinterpret_cast<uint8_t*>(align_up(reinterpret_cast<uintptr_t>(workspace), 256));
     float* logits = reinterpret_cast<float*>(base + dispatch_logits_offset(T, topk, n_experts, hidden));

@@ -76,7 +76,7 @@ size_t mxfp4_grouped_workspace_bytes(int n_exp, int hidden, int out_dim);
  * ids[t, :] = top-`topk` expert indices of logits[t, :] (descending, ties to
  * the lower index); weights[t, k] = sigmoid(l_k) / sum_k' sigmoid(l_k').
  * Returns 0; -1 bad T/n_experts/topk (T<1, n_experts<1 or >1024, topk<1 or
- * > min(n_experts, 16)); -5 launch failure. */
+ * > min(n_experts, 16)); -10 logits, ids or weights null; -5 launch failure. */
 int mxfp4_moe_route_sigmoid_topk(const float* logits, int T, int n_experts, int topk,
                                  int32_t* ids, float* weights, hipStream_t stream);
 
@@ -96,8 +96,8 @@ int mxfp4_moe_route_sigmoid_topk(const float* logits, int T, int n_experts, int 
  * numbers exist; here NaN entries then fill the last picks). Replaces the
  * sqrt_softplus_kernel launch, the D2H copy, the stream sync and
  * topk6_norm_scale_host of routed.cu:156-208, 418-446. Returns 0; -1 bad
- * T/n_experts/topk/score_mode (as mxfp4_moe_route_sigmoid_topk); -5 launch
- * failure. */
+ * T/n_experts/topk/score_mode (as mxfp4_moe_route_sigmoid_topk); -10 logits,
+ * ids or weights null; -5 launch failure. */
 int mxfp4_moe_route_topk(const float* logits, int T, int n_experts, int topk, int score_mode,
                          float routed_scale, int32_t* ids, float* weights, hipStream_t stream);
 
@@ -124,7 +124,10 @@ size_t mxfp4_moe_workspace_bytes(int T, int topk, int n_experts, int hidden);
  * x [T, K_in] bf16, ids/weights [T, topk], out [T, out_dim] bf16.
  * Returns 0; -1 K_in%32; -2 hidden%32; -3 K_in/hidden > 4096; -4 bad
  * T/topk/n_experts (T<1 or >64, topk<1 or >16, n_experts<1 or >1024);
- * -5/-6/-7 launch failure of routing/stage A/stage B. An id outside
+ * -5/-6/-7 launch failure of routing/stage A/stage B; -10 a required pointer
+ * is null (checked after the shapes, before any launch; the entries below
+ * that return "as mxfp4_moe_grouped_gemv" or "as mxfp4_moe_layer" do the
+ * same, ids_out and weights_out being optional). An id outside
  * [0, n_experts) is skipped (contributes nothing). */
 int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x,
                            const uint8_t* W1_packed, const uint8_t* W3_packed,

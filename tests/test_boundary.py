@@ -167,6 +167,48 @@ def test_noalloc_validation_codes():
     assert wb(16, 8, 256, 2048) <= 4 << 20                 # the configuration's T <= 16 fits
 
 
+def test_moe_extensions_reject_null_operands():
+    """Every routed-MoE extension returns -10 when a required pointer is null,
+    after the shape checks and before any HIP call (one pointer null at a
+    time, the others set to an address that is never dereferenced); the
+    optional ids_out / weights_out of the layer entries are not required."""
+    lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
+    P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    D = ctypes.c_void_p(1 << 20)   # stand-in address; validation never reads it
+
+    def each_null(fn, argtypes, build, n_ptr):
+        fn.restype = I
+        fn.argtypes = argtypes
+        for i in range(n_ptr):
+            ptrs = [D] * n_ptr
+            ptrs[i] = N
+            assert fn(*build(ptrs)) == -10, f"{fn.__name__}: pointer {i}"
+
+    shape = (1, 8, 256, 4096, 2048, 4096)       # T, topk, n_experts, K_in, hidden, out_dim
+    each_null(lib.mxfp4_moe_grouped_gemv, [P] * 9 + [I] * 6 + [P] * 3,
+              lambda p: p[:9] + list(shape) + p[9:] + [N], 11)
+    each_null(lib.mxfp4_moe_grouped_gemv_noalloc, [P] * 9 + [I] * 6 + [P] * 2,
+              lambda p: p[:9] + list(shape) + p[9:] + [N], 10)
+    # x, logits, W1..S2 (8), out, workspace; ids_out / weights_out stay null
+    each_null(lib.mxfp4_moe_layer, [P] * 8 + [I] * 6 + [P] * 5,
+              lambda p: p[:8] + list(shape) + [p[8], N, N, p[9], N], 10)
+    each_null(lib.mxfp4_moe_gate_swiglu, [P] * 6 + [I] * 5 + [P] * 4,
+              lambda p: p[:6] + list(shape[:5]) + [N, N, p[6], N], 7)
+    each_null(lib.mxfp4_moe_build_routing, [P, P] + [I] * 4 + [P, P],
+              lambda p: [p[0], p[1], 1, 8, 256, 2048, p[2], N], 3)
+    each_null(lib.mxfp4_moe_swiglu, [P] * 5 + [I] * 5 + [P, P],
+              lambda p: p[:5] + list(shape[:5]) + [p[5], N], 6)
+    each_null(lib.mxfp4_moe_down, [P, P] + [I] * 5 + [P, P, P],
+              lambda p: [p[0], p[1], 1, 8, 256, 2048, 4096, p[2], p[3], N], 4)
+    each_null(lib.mxfp4_moe_route_sigmoid_topk, [P, I, I, I, P, P, P],
+              lambda p: [p[0], 1, 256, 8, p[1], p[2], N], 3)
+    each_null(lib.mxfp4_moe_route_topk, [P, I, I, I, I, F, P, P, P],
+              lambda p: [p[0], 1, 256, 6, 1, 1.5, p[1], p[2], N], 3)
+    # x, W_gate, W1..S2 (6), out, workspace; ids_out / weights_out stay null
+    each_null(lib.mxfp4_moe_routed_dispatch, [P] * 8 + [I] * 6 + [F] + [P] * 5,
+              lambda p: p[:8] + [1, 6, 256, 4096, 2048, 4096, 1.5, p[8], N, N, p[9], N], 10)
+
+
 def test_router_and_dispatch_validation_codes():
     lib = _lib("mxfp4-routed/libmxfp4_grouped_gemv.so")
     P, I = ctypes.c_void_p, ctypes.c_int
@@ -206,7 +248,7 @@ def test_router_and_dispatch_validation_codes():
     assert call(1, 6, 256, 8192, 2048, 4096) == -3
     assert call(1, 300, 256, 4096, 2048, 4096) == -4
     assert call(1, 8, 4, 4096, 2048, 4096) == -4          # topk > n_experts
-    assert call(1, 6, 256, 4096, 2048, 4096) == -3        # null operands
+    assert call(1, 6, 256, 4096, 2048, 4096) == -10       # null operands
     pd = lib.mxfp4_moe_prefill_dequant_bf16
     pd.restype = I
     pd.argtypes = [P, P, I, I, P, P]
