@@ -16,6 +16,7 @@
 // kernel/fp8-dense/fp8_e4m3_gemv.cu:148-154.
 
 #include <cstdio>
+#include <initializer_list>
 
 #include "dsv4_device.h"
 #include "dsv4_kernels.h"
@@ -693,6 +694,20 @@ __global__ __launch_bounds__(256) void fp8_dequant_kernel(const uint8_t* w, cons
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The extensions reject a null operand before any launch; the drop-in
+// fp8_e4m3_gemv_m1 keeps the reference's checks (shapes only).
+constexpr int kNullOperand = -10;
+
+bool operands_set(const char* who, std::initializer_list<const void*> ps) {
+    for (const void* p : ps) {
+        if (p == nullptr) {
+            std::fprintf(stderr, "%s: a required pointer is null\n", who);
+            return false;
+        }
+    }
+    return true;
+}
+
 int validate(int K, int N) {
     if (K % kTile != 0 || K < kTile) {
         std::fprintf(stderr, "fp8_e4m3_gemv: K=%d not a positive multiple of %d\n", K, kTile);
@@ -927,6 +942,7 @@ extern "C" int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const u
         std::fprintf(stderr, "fp8_e4m3_gemv: T=%d outside [1, %d]\n", T, kMaxT);
         return -5;
     }
+    if (!operands_set("fp8_e4m3_gemv", {x, W_fp8, W_scale, y})) return kNullOperand;
     Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W_fp8, W_scale, K, N, T,
               weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y),
               y_row_stride, 0, 0};
@@ -948,6 +964,7 @@ extern "C" int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride,
         std::fprintf(stderr, "fp8_e4m3_gemv_grouped: G=%d outside [1, 65535]\n", G);
         return -6;
     }
+    if (!operands_set("fp8_e4m3_gemv_grouped", {x, W_fp8, W_scale, y})) return kNullOperand;
     Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W_fp8, W_scale, K, N, T,
               weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y),
               y_row_stride, x_group_stride, y_group_stride};
@@ -971,6 +988,9 @@ extern "C" int fp8_e4m3_gemv_multi(const dsv4_bf16_t* x, int64_t x_row_stride, i
         std::fprintf(stderr, "fp8_e4m3_gemv_multi: T=%d outside [1, %d]\n", T, kMaxT);
         return -5;
     }
+    if (!operands_set("fp8_e4m3_gemv_multi", {x})) return kNullOperand;
+    for (int m = 0; m < n_mats; ++m)
+        if (!operands_set("fp8_e4m3_gemv_multi", {W_fp8[m], W_scale[m], y[m]})) return kNullOperand;
     MultiArgs ma{};
     ma.base = Fp8Args{reinterpret_cast<const uint16_t*>(x), x_row_stride, nullptr, nullptr, K, 0, T, 0, 0,
                       nullptr, 0, 0, 0};
@@ -1044,6 +1064,7 @@ extern "C" int fp8_e4m3_swiglu_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, 
                              "W1, W3 and rows\n");
         return -6;
     }
+    if (!operands_set("fp8_e4m3_swiglu_gemv", {x, W1_fp8, W1_scale, W3_fp8, W3_scale, act})) return kNullOperand;
     const SwigluArgs sw{W3_fp8, W3_scale, limit, clamp_up};
     if (use_mfma(T, K, N, x_row_stride)) {
         const hipError_t e = launch_mfma<2>(a, sw, 1, stream);
@@ -1075,6 +1096,7 @@ extern "C" int fp8_e4m3_dequant_bf16(const uint8_t* W_fp8, const uint8_t* W_scal
                                      hipStream_t stream) {
     if (K % kTile != 0 || K < kTile) return -1;
     if (N < 1) return -4;
+    if (!operands_set("fp8_e4m3_dequant_bf16", {W_fp8, W_scale, out})) return kNullOperand;
     const int64_t total = (int64_t)N * (K / 16);
     hipLaunchKernelGGL(fp8_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        stream, W_fp8, W_scale, K, N, weight_row_stride_bytes,
@@ -1109,6 +1131,7 @@ extern "C" int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* re
                              "x_norm, and new_residual with a residual\n");
         return -6;
     }
+    if (!operands_set("fp8_e4m3_rmsnorm_gemv", {x, W_fp8, W_scale, y})) return kNullOperand;
     const NormArgs nm{reinterpret_cast<const uint16_t*>(residual), reinterpret_cast<const uint16_t*>(norm_weight),
                       eps, reinterpret_cast<uint16_t*>(x_norm), reinterpret_cast<uint16_t*>(new_residual)};
     const int KC = K / 16;

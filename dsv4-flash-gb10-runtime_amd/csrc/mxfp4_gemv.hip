@@ -262,6 +262,10 @@ extern "C" int mxfp4_dequant_bf16(const uint8_t* W_packed, const uint8_t* W_scal
                                   dsv4_bf16_t* out, hipStream_t stream) {
     if (K % kBlkElems != 0 || K < kBlkElems) return -1;
     if (N < 1) return -3;
+    if (!W_packed || !W_scale || !out) {
+        std::fprintf(stderr, "mxfp4_dequant_bf16: a required pointer is null\n");
+        return -10;
+    }
     const int64_t total = (int64_t)N * (K / kBlkElems);
     const dim3 grid((unsigned)((total + 255) / 256));
     hipLaunchKernelGGL(mxfp4_dequant_kernel, grid, dim3(256), 0, stream, W_packed, W_scale, K, N,

@@ -270,7 +270,8 @@ int mxfp4_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_packed, const uint8_t* 
 /* EXTENSION (debug): out[n,k] = bf16( e2m1(W[n,k]) * 2^(S[n,k/32]-127) ), using
  * the same device decode routine as the GEMVs, so a bit-exact comparison with
  * the reference dequant (runtime/mxfp4_loader.py:272-309) checks the kernels'
- * decode. out is [N, K] contiguous. Returns 0; -1 K%32; -3 launch failure. */
+ * decode. out is [N, K] contiguous. Returns 0; -1 K%32; -3 N < 1 or launch
+ * failure; -10 W_packed, W_scale or out null. */
 int mxfp4_dequant_bf16(const uint8_t* W_packed, const uint8_t* W_scale, int K, int N,
                        int64_t packed_row_stride_bytes, int64_t scale_row_stride_bytes,
                        dsv4_bf16_t* out, hipStream_t stream);
@@ -298,7 +299,9 @@ int fp8_e4m3_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_fp8, const uint8_t* 
  * aligned operands it runs on the matrix cores (bf16 MFMA on the exact E4M3
  * values) from T = 4 at N >= 2048, from T = 9 at N >= 1024 and from T = 2 at
  * K = 8192, on the vector units otherwise; the two paths agree within fp32
- * rounding of the sums. Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16. */
+ * rounding of the sums. Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16
+ * and -10 for a null x, W_fp8, W_scale or y (after the shape checks, before
+ * any launch; the other FP8 extensions likewise for their operands). */
 int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
                   const uint8_t* W_scale, int K, int N, int T,
                   int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
@@ -380,7 +383,8 @@ int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* residual,
 
 /* EXTENSION (debug): out[n,k] = bf16( e4m3(W[n,k]) * 2^(S[n/128,k/128]-127) ),
  * the device decode of the FP8 GEMVs, for the bit-exact check against
- * runtime/dsv4_engine_mxfp4.py:531-553. Returns 0; -1 K%128; -4 launch failure. */
+ * runtime/dsv4_engine_mxfp4.py:531-553. Returns 0; -1 K%128; -4 N < 1 or
+ * launch failure; -10 W_fp8, W_scale or out null. */
 int fp8_e4m3_dequant_bf16(const uint8_t* W_fp8, const uint8_t* W_scale, int K, int N,
                           int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
                           dsv4_bf16_t* out, hipStream_t stream);

@@ -348,6 +348,50 @@ def test_fp8_validation_codes():
     assert rn(N, N, N, 1e-6, N, N, 4096, 1536, 1, 4096, 32, N, None, N, N) == -6  # no x_norm
 
 
+def test_fp8_and_dequant_extensions_reject_null_operands():
+    """The FP8 extensions and the dense MXFP4 dequant return -10 when an
+    operand pointer is null, after the shape checks and before any HIP call
+    (one pointer null at a time; the others a 16-byte aligned address that is
+    never dereferenced)."""
+    fl = _lib("fp8-dense/libfp8_e4m3_gemv.so")
+    P, I, L, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    D = ctypes.c_void_p(1 << 20)
+
+    def each_null(fn, argtypes, build, n_ptr):
+        fn.restype = I
+        fn.argtypes = argtypes
+        for i in range(n_ptr):
+            ptrs = [D] * n_ptr
+            ptrs[i] = N
+            assert fn(*build(ptrs)) == -10, f"{fn.__name__}: pointer {i}"
+
+    each_null(fl.fp8_e4m3_gemv, [P, L, P, P, I, I, I, L, L, P, L, P],
+              lambda p: [p[0], 4096, p[1], p[2], 4096, 1536, 2, 4096, 32, p[3], 1536, N], 4)
+    each_null(fl.fp8_e4m3_gemv_grouped, [P, L, L, P, P, I, I, I, I, L, L, P, L, L, P],
+              lambda p: [p[0], 32768, 4096, p[1], p[2], 8, 4096, 1024, 1, 4096, 32, p[3], 8192, 1024, N], 4)
+    each_null(fl.fp8_e4m3_swiglu_gemv, [P, L, P, P, P, P, I, I, I, L, L, F, I, P, L, P],
+              lambda p: [p[0], 4096, p[1], p[2], p[3], p[4], 4096, 2048, 1, 4096, 32, 10.0, 1, p[5], 2048, N], 6)
+    # x, W, S, y; norm_weight and x_norm set, no residual
+    each_null(fl.fp8_e4m3_rmsnorm_gemv, [P, P, P, F, P, P, I, I, I, L, L, P, P, P, P],
+              lambda p: [p[0], N, D, 1e-6, p[1], p[2], 4096, 1536, 1, 4096, 32, p[3], D, N, N], 4)
+    each_null(fl.fp8_e4m3_dequant_bf16, [P, P, I, I, L, L, P, P],
+              lambda p: [p[0], p[1], 4096, 1536, 4096, 32, p[2], N], 3)
+    mu = fl.fp8_e4m3_gemv_multi
+    mu.restype = I
+    mu.argtypes = [P, L, I, I, I] + [P] * 7 + [P]
+    Ns = (ctypes.c_int * 2)(1024, 512)
+    strides = (ctypes.c_int64 * 2)(4096, 4096)
+    full = (ctypes.c_void_p * 2)(1 << 20, 1 << 21)
+    holed = (ctypes.c_void_p * 2)(1 << 20, None)
+    assert mu(N, 4096, 4096, 1, 2, full, full, Ns, strides, strides, full, strides, N) == -10     # x
+    assert mu(D, 4096, 4096, 1, 2, holed, full, Ns, strides, strides, full, strides, N) == -10    # W[1]
+    assert mu(D, 4096, 4096, 1, 2, full, holed, Ns, strides, strides, full, strides, N) == -10    # S[1]
+    assert mu(D, 4096, 4096, 1, 2, full, full, Ns, strides, strides, holed, strides, N) == -10    # y[1]
+    ml = _lib("mxfp4-dense/libmxfp4_gemv.so")
+    each_null(ml.mxfp4_dequant_bf16, [P, P, I, I, L, L, P, P],
+              lambda p: [p[0], p[1], 4096, 2048, 2048, 128, p[2], N], 3)
+
+
 def test_rmsnorm_validation_codes():
     lib = _lib("rmsnorm-fuse/librmsnorm_fuse.so")
     f = lib.rmsnorm_fuse_fwd
