@@ -498,10 +498,12 @@ __global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const Mult
 // RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
 //   v = x + residual (fp32; or x alone), new_residual = bf16(v),
 //   x_norm = bf16( (g * bf16(v)) * rsqrt(sum(v^2) / K + eps) ),  y = W . x_norm
-// with the bits of librmsnorm_fuse's kernels: each of the 256 threads sums
-// the squares of the same 8-element chunks (t, t+256) in the same order,
-// the per-wave sums are added in wave order, and every element is normalised
-// by the same expression. The thread then normalises its own 16-element GEMV
+// with the bits of librmsnorm_fuse's kernels, which give each thread one
+// 8-element piece and add the wave sums in wave order: thread t here holds
+// pieces t and t + 256, sums the squares of each piece on its own, reduces
+// each over its wave (those are the library's waves w and w + 4), and the
+// 4 or 8 wave totals are added in the library's order; every element is
+// normalised by the same expression. The thread then normalises its own 16-element GEMV
 // slice and proceeds as fp8_gemv_tile_kernel. Workgroup 0 writes x_norm and
 // new_residual. The loads are issued activation, residual and weight-scale
 // slices first, then the weights, so the norm is computed while the weights
@@ -530,7 +532,7 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
     constexpr int kVals = C * TT;
     constexpr int kNV = KC / 128;               // 8-element chunks per thread in the norm's order
     __shared__ float part[kWaves][C][TT];
-    __shared__ float red[TT][kWaves];
+    __shared__ float red[TT][kWaves * kNV];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -571,23 +573,24 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // Sum of squares per token, in the order of rmsnorm_vec_kernel.
+    // Sum of squares per token, in the order of rmsnorm_vec_kernel: piece
+    // t + 256c belongs to the library's wave (wave + 4c).
 #pragma unroll
     for (int tok = 0; tok < TT; ++tok) {
-        float ss = 0.f;
 #pragma unroll
         for (int c = 0; c < kNV; ++c) {
             float xa[8], ra[8];
             unpack8_f32(px[tok][c], xa);
             if constexpr (RESID) unpack8_f32(pr[tok][c], ra);
+            float ss = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v = RESID ? xa[e] + ra[e] : xa[e];
                 ss = fmaf(v, v, ss);
             }
+            ss = wave_sum(ss);
+            if (lane == 0) red[tok][wave + kWaves * c] = ss;
         }
-        ss = wave_sum(ss);
-        if (lane == 0) red[tok][wave] = ss;
     }
     __syncthreads();
     const bool writer = blockIdx.x == 0 && t < KC;
@@ -599,7 +602,7 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
     for (int tok = 0; tok < TT; ++tok) {
         float total = 0.f;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) total += red[tok][w2];
+        for (int w2 = 0; w2 < kWaves * kNV; ++w2) total += red[tok][w2];
         const float rms = rsqrtf(total * (1.0f / (float)K) + nm.eps);
         float xa[16], ra[16];
         unpack8_f32(sx[tok][0], xa);

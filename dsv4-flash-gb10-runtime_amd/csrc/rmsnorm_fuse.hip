@@ -6,11 +6,12 @@
 // The sum of squares runs over the unrounded fp32 t and the product order
 // (w * v) * rms follows reference kernel/rmsnorm-fuse/rmsnorm_fuse.cu:138-155.
 //
-// One workgroup (256 threads = 4 waves) per row. Each thread keeps its slice
-// of the row in registers (8 bf16 per 16-byte load, at most 32 values per
-// thread for H <= 8192), so the row is read once; the sum of squares is
-// reduced with wave shuffles and a 4-entry LDS exchange. The norm weight is
-// loaded together with the row, before the reduction.
+// One workgroup per row. On the vector path each thread holds one 16-byte
+// piece (8 bf16) of the row, of the residual and of the weight, all loaded
+// together before the reduction, so the row is read once; the workgroup has
+// 4, 8 or 16 waves, enough for one piece per thread. The sum of squares is
+// reduced with wave shuffles, then the wave totals are added in wave order
+// through LDS.
 
 #include <cstdint>
 
@@ -21,11 +22,14 @@ namespace {
 
 using namespace dsv4;
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;                          // scalar path
 constexpr int kMaxHidden = 8192;                       // reference RMSF_MAX_HIDDEN
 constexpr int kVec = 8;                                // bf16 per 16-byte access
-constexpr int kMaxVecPerThread = kMaxHidden / (kThreads * kVec);  // 4
+constexpr int kMaxVecWaves = kMaxHidden / (kVec * 64); // 16
 
+// Sum of v over the workgroup's W waves: a shuffle reduction in each wave,
+// then the wave totals added in wave order.
+template <int W>
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
     const int lane = threadIdx.x & 63;
@@ -34,7 +38,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     __syncthreads();
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+    for (int w = 0; w < W; ++w) s += red[w];
     return s;
 }
 
@@ -53,81 +57,80 @@ __device__ __forceinline__ u32x4 pack8(const uint16_t* h) {
     return r;
 }
 
-// Vector path: rows 16-byte aligned and H % 8 == 0; NV = ceil(H / 2048)
-// 16-byte pieces per thread. Every load (row, residual and weight pieces) is
-// issued up front, unconditionally (indices clamped into the row), so the
-// weight is in flight with the row and the whole kernel waits on one memory
-// round trip before the reduction.
-template <bool RESID, int NV>
-__global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const uint16_t* x, const uint16_t* res,
-                                                               const uint16_t* w, uint16_t* y,
-                                                               uint16_t* new_res, int hidden,
-                                                               float eps) {
-    __shared__ float red[kThreads / 64];
+// Vector path: rows 16-byte aligned and H % 8 == 0. Thread i holds piece i
+// (elements 8i .. 8i+7) of a block of W = 4, 8 or 16 waves (H up to 2048,
+// 4096, 8192); threads past the row load piece H/8 - 1 and contribute
+// nothing. Every load (row, residual and weight) is issued up front, so the
+// kernel waits on one memory round trip before the reduction. One piece per
+// thread measured fastest on MI355X (HIP-graph replay, residual entry, T = 1):
+// 2.66 us at H = 4096 against 3.25 with two pieces per thread of 256 threads,
+// and 3.34 us at H = 8192 against 3.76 (512 threads) and 4.72 (256). A wave
+// count chosen at run time (a loop over it in the block sum) was 2-6% slower.
+template <bool RESID, int W>
+__global__ __launch_bounds__(64 * W) void rmsnorm_vec_kernel(const uint16_t* x, const uint16_t* res,
+                                                                        const uint16_t* w, uint16_t* y,
+                                                                        uint16_t* new_res, int hidden,
+                                                                        float eps) {
+    __shared__ float red[W];
     const int64_t off = (int64_t)blockIdx.x * hidden;
     const int nvec = hidden / kVec;
-    u32x4 xv[NV], rv[NV], gv[NV];
-#pragma unroll
-    for (int c = 0; c < NV; ++c) {
-        const int64_t i = min((int)threadIdx.x + c * kThreads, nvec - 1);
-        xv[c] = *reinterpret_cast<const u32x4*>(x + off + i * kVec);
-        if constexpr (RESID) rv[c] = *reinterpret_cast<const u32x4*>(res + off + i * kVec);
-        gv[c] = *reinterpret_cast<const u32x4*>(w + i * kVec);
-    }
-    float v[NV][kVec];
+    const int i = threadIdx.x;
+    const int ic = min(i, nvec - 1);
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(x + off + (int64_t)ic * kVec);
+    u32x4 rv{};
+    if constexpr (RESID) rv = *reinterpret_cast<const u32x4*>(res + off + (int64_t)ic * kVec);
+    const u32x4 gv = *reinterpret_cast<const u32x4*>(w + (int64_t)ic * kVec);
+    float v[kVec];
     float ss = 0.f;
+    if (i < nvec) {
+        float a[kVec];
+        unpack8(xv, a);
+        if constexpr (RESID) {
+            float b[kVec];
+            unpack8(rv, b);
+            uint16_t tb[kVec];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) {
-        const int i = threadIdx.x + c * kThreads;
-        if (i < nvec) {
-            float a[kVec];
-            unpack8(xv[c], a);
-            if constexpr (RESID) {
-                float b[kVec];
-                unpack8(rv[c], b);
-                uint16_t tb[kVec];
+            for (int e = 0; e < kVec; ++e) {
+                const float t = a[e] + b[e];
+                ss = fmaf(t, t, ss);
+                tb[e] = f32_to_bf16_bits(t);
+                v[e] = bf16_bits_to_f32(tb[e]);
+            }
+            *reinterpret_cast<u32x4*>(new_res + off + (int64_t)i * kVec) = pack8(tb);
+        } else {
 #pragma unroll
-                for (int e = 0; e < kVec; ++e) {
-                    const float t = a[e] + b[e];
-                    ss = fmaf(t, t, ss);
-                    tb[e] = f32_to_bf16_bits(t);
-                    v[c][e] = bf16_bits_to_f32(tb[e]);
-                }
-                *reinterpret_cast<u32x4*>(new_res + off + (int64_t)i * kVec) = pack8(tb);
-            } else {
-#pragma unroll
-                for (int e = 0; e < kVec; ++e) {
-                    ss = fmaf(a[e], a[e], ss);
-                    v[c][e] = a[e];
-                }
+            for (int e = 0; e < kVec; ++e) {
+                ss = fmaf(a[e], a[e], ss);
+                v[e] = a[e];
             }
         }
     }
-    const float total = block_sum(ss, red);
+    const float total = block_sum<W>(ss, red);
     const float rms = rsqrtf(total * (1.0f / (float)hidden) + eps);
+    if (i < nvec) {
+        float g[kVec];
+        unpack8(gv, g);
+        uint16_t o[kVec];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) {
-        const int i = threadIdx.x + c * kThreads;
-        if (i < nvec) {
-            float g[kVec];
-            unpack8(gv[c], g);
-            uint16_t o[kVec];
-#pragma unroll
-            for (int e = 0; e < kVec; ++e) o[e] = f32_to_bf16_bits((g[e] * v[c][e]) * rms);
-            *reinterpret_cast<u32x4*>(y + off + (int64_t)i * kVec) = pack8(o);
-        }
+        for (int e = 0; e < kVec; ++e) o[e] = f32_to_bf16_bits((g[e] * v[e]) * rms);
+        *reinterpret_cast<u32x4*>(y + off + (int64_t)i * kVec) = pack8(o);
     }
 }
 
 template <bool RESID>
 void launch_vec(const uint16_t* x, const uint16_t* res, const uint16_t* w, uint16_t* y, uint16_t* new_res,
                 int n_rows, int hidden, float eps, hipStream_t stream) {
-    const int nv = (hidden / kVec + kThreads - 1) / kThreads;
-    const dim3 grid((unsigned)n_rows), block(kThreads);
-    if (nv <= 1) hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 1>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
-    else if (nv == 2) hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 2>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
-    else if (nv == 3) hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 3>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
-    else hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 4>), grid, block, 0, stream, x, res, w, y, new_res, hidden, eps);
+    const int pieces = hidden / kVec;              // <= 1024 for hidden <= 8192
+    const dim3 grid((unsigned)n_rows);
+    if (pieces <= 256)
+        hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 4>), grid, dim3(256), 0, stream, x, res, w, y, new_res, hidden,
+                           eps);
+    else if (pieces <= 512)
+        hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, 8>), grid, dim3(512), 0, stream, x, res, w, y, new_res, hidden,
+                           eps);
+    else
+        hipLaunchKernelGGL((rmsnorm_vec_kernel<RESID, kMaxVecWaves>), grid, dim3(1024), 0, stream, x, res, w, y,
+                           new_res, hidden, eps);
 }
 
 // Scalar path for any alignment / H: each thread walks h = tid, tid+256, ...
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_scalar_kernel(const uint16_t
             }
         }
     }
-    const float total = block_sum(ss, red);
+    const float total = block_sum<kThreads / 64>(ss, red);
     const float rms = rsqrtf(total * (1.0f / (float)hidden) + eps);
 #pragma unroll
     for (int c = 0; c < kPer; ++c) {

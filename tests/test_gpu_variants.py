@@ -11,7 +11,8 @@ and operand alignment and that the configuration-shaped tests do not reach:
   unaligned; the routed layer's general stage-A and stage-B kernels, which take
   over when scale rows, the activation or W2 are not 16-byte aligned, for one
   and two blocks per lane; the router GEMV at K = 8192;
-- RMSNorm: three pieces per thread (hidden 6144) and the scalar forward path.
+- RMSNorm: hidden 6144 (16 waves with a quarter of the threads past the row)
+  and the scalar forward path.
 
 Every case is checked against the oracle (max rel err <= 1e-2, cosine >=
 0.9999); where two launches must agree, bit for bit."""
@@ -272,9 +273,10 @@ def test_router_logits_longest_rows(device):
 
 # ---------------------------------------------------------------- RMSNorm ---
 
-def test_rmsnorm_three_pieces_and_scalar_forward(device):
-    """hidden = 6144 (three 16-byte pieces per thread) through both entries,
-    and the forward entry on its scalar path (hidden not a multiple of 8)."""
+def test_rmsnorm_partial_block_and_scalar_forward(device):
+    """hidden = 6144 (768 pieces in a 1,024-thread block: the last 256 threads
+    hold no piece) through both entries, and the forward entry on its scalar
+    path (hidden not a multiple of 8)."""
     for H, T in ((6144, 3), (4001, 2)):
         announce(f"rmsnorm H={H} T={T}")
         h = synth.normal_bf16(21600 + H, (T, H))
