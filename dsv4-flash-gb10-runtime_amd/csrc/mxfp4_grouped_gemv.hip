@@ -1573,41 +1573,58 @@ __global__ __launch_bounds__(64) void moe_route_topk_kernel(const float* logits,
 
 // Router gate GEMV (reference kernel/cpp-engine-mxfp4/routed.cu:124-153):
 //   logits[t, n] = sum_k Wg[n, k] * x[t, k],  bf16 operands, fp32 accumulate.
-// One wave per gate row; lane l owns the 16-byte pieces l, l+64, ... of the
-// row (each load instruction reads one contiguous KiB), which stay in
-// registers while the T tokens' activation pieces (L2 hits after the first
-// wave) are dotted against them with v_dot2_f32_bf16; the lane sums are
-// reduced over the wave. Pieces past the row (K not a multiple of 512) are
-// loaded clamped and multiplied by zero activations. One wave per workgroup
-// (256 workgroups for 256 experts): 3.14 µs for 256 x 4096 against 3.21 with
-// two waves and 3.42 with four.
-constexpr int kRouterWaves = 1;
+// One workgroup per gate row (expert), its kRouterWaves waves splitting the
+// row: wave s owns the 64*NJS consecutive 16-byte pieces from 64*NJS*s, lane
+// l the pieces 64*(NJS*s + j) + l (each load instruction reads one
+// contiguous KiB). The pieces stay in registers while the T tokens'
+// activation pieces (L2 hits after the first workgroups) are dotted against
+// them with v_dot2_f32_bf16; each wave reduces its sums, and the wave sums
+// meet in LDS and are added in wave order. Pieces past the row (K not a
+// multiple of 512) are loaded clamped and multiplied by zero activations.
+// Four waves per row measured fastest on MI355X for 256 x 4096 (HIP-graph
+// replay, weights rotated over 512 MB): 2.44 us at T = 1 and 3.55 at T = 4,
+// against 3.13 and 6.40 with one wave per row, 2.45 / 3.63 with two and
+// 2.47 / 3.53 with eight.
+constexpr int kRouterWaves = 4;
+constexpr int kRouterMaxT = 64;
 
 template <int NJ>
 __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_gemv_kernel(const uint16_t* x, const uint16_t* wg,
                                                                             int T, int n_rows, int K,
                                                                             float* logits) {
+    static_assert(NJ % kRouterWaves == 0, "whole pieces per wave");
+    static_assert(kRouterMaxT >= kMaxTokens, "one LDS row per token");
+    constexpr int NJS = NJ / kRouterWaves;
+    __shared__ float part[kRouterMaxT][kRouterWaves];
     const int lane = threadIdx.x & 63;
-    const int row = min((int)(blockIdx.x * kRouterWaves + (threadIdx.x >> 6)), n_rows - 1);
+    const int s = threadIdx.x >> 6;
+    const int row = min((int)blockIdx.x, n_rows - 1);
     const int npc = K / 8;                     // 16-byte pieces per row
     const uint16_t* wr = wg + (int64_t)row * K;
-    u32x4 w[NJ];
+    u32x4 w[NJS];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) w[j] = ld16_stream(reinterpret_cast<const uint8_t*>(wr + 8 * min(lane + 64 * j, npc - 1)));
+    for (int j = 0; j < NJS; ++j)
+        w[j] = ld16_stream(reinterpret_cast<const uint8_t*>(wr + 8 * min(64 * (NJS * s + j) + lane, npc - 1)));
     for (int t = 0; t < T; ++t) {
         const uint16_t* xt = x + (int64_t)t * K;
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int pc = lane + 64 * j;
+        for (int j = 0; j < NJS; ++j) {
+            const int pc = 64 * (NJS * s + j) + lane;
             u32x4 xv = *reinterpret_cast<const u32x4*>(xt + 8 * min(pc, npc - 1));
             if (pc >= npc) xv = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc = dot2(as_bf16x2(w[j][q]), as_bf16x2(xv[q]), acc);
         }
         acc = wave_sum(acc);
-        if (lane == 0 && blockIdx.x * kRouterWaves + (threadIdx.x >> 6) < (unsigned)n_rows)
-            logits[(int64_t)t * n_rows + row] = acc;
+        if (lane == 0) part[t][s] = acc;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < T) {
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < kRouterWaves; ++q) sum += part[threadIdx.x][q];
+        logits[(int64_t)threadIdx.x * n_rows + row] = sum;
     }
 }
 
@@ -1911,7 +1928,7 @@ int launch_router(const dsv4_bf16_t* x, const dsv4_bf16_t* W_gate, int T, int n_
         std::fprintf(stderr, "mxfp4 router: x, W_gate and logits must be non-null, x and W_gate 16-byte aligned\n");
         return -3;
     }
-    const dim3 grid((unsigned)((n_experts + kRouterWaves - 1) / kRouterWaves)), block(64 * kRouterWaves);
+    const dim3 grid((unsigned)n_experts), block(64 * kRouterWaves);
     const auto* xp = reinterpret_cast<const uint16_t*>(x);
     const auto* wp = reinterpret_cast<const uint16_t*>(W_gate);
     const int nj = (K / 8 + 63) / 64;
