@@ -498,12 +498,16 @@ __global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const Mult
 // RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
 //   v = x + residual (fp32; or x alone), new_residual = bf16(v),
 //   x_norm = bf16( (g * bf16(v)) * rsqrt(sum(v^2) / K + eps) ),  y = W . x_norm
-// with the bits of librmsnorm_fuse's kernels, which give each thread one
-// 8-element piece and add the wave sums in wave order: thread t here holds
-// pieces t and t + 256, sums the squares of each piece on its own, reduces
-// each over its wave (those are the library's waves w and w + 4), and the
-// 4 or 8 wave totals are added in the library's order; every element is
-// normalised by the same expression. The thread then normalises its own 16-element GEMV
+// with the bits of librmsnorm_fuse's kernels. The library gives thread q
+// the 8-element piece q and reduces each wave's 64 sums of squares with the
+// xor butterfly (lane distances 32, 16, ..., 1), then adds the wave totals
+// in order. Here thread t's GEMV slice is pieces p = 2(t % KC) and p + 1, so
+// the row is read once: lanes j of a wave hold the library's lanes 2j and
+// 2j + 1 (mod 64) of waves 2w' and 2w' + 1 (lanes 0-31 and 32-63). The
+// library's steps at distance 32 .. 2 pair those lanes' j ^ 16 .. j ^ 1 with
+// the same piece slot, and its last step adds the two slots of one lane: the
+// same additions on the same operands. Every element is then normalised by
+// the same expression. The thread then normalises its own 16-element GEMV
 // slice and proceeds as fp8_gemv_tile_kernel. Workgroup 0 writes x_norm and
 // new_residual. The loads are issued activation, residual and weight-scale
 // slices first, then the weights, so the norm is computed while the weights
@@ -540,18 +544,11 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
     const int k = 16 * (t % KC);
     const int K = a.K;
 
-    // The norm's chunks, then the GEMV slice of x, residual and g.
-    u32x4 px[TT][kNV], pr[TT][kNV];
+    // The GEMV slice of x, residual and g (the norm reads the same pieces).
     u32x4 sx[TT][2], sr[TT][2], sg[2];
 #pragma unroll
     for (int tok = 0; tok < TT; ++tok) {
         const int64_t row = (int64_t)min(tok, a.T - 1) * K;
-#pragma unroll
-        for (int c = 0; c < kNV; ++c) {
-            const int64_t e = row + 8 * (t + 256 * c);
-            px[tok][c] = *reinterpret_cast<const u32x4*>(a.x + e);
-            if constexpr (RESID) pr[tok][c] = *reinterpret_cast<const u32x4*>(nm.res + e);
-        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             sx[tok][h] = *reinterpret_cast<const u32x4*>(a.x + row + k + 8 * h);
@@ -573,24 +570,29 @@ __global__ __launch_bounds__(256) void fp8_norm_gemv_tile_kernel(const Fp8Args a
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // Sum of squares per token, in the order of rmsnorm_vec_kernel: piece
-    // t + 256c belongs to the library's wave (wave + 4c).
+    // Sum of squares per token, in the order of rmsnorm_vec_kernel (above):
+    // this wave's lanes 0-31 and 32-63 end with the totals of the library's
+    // waves 2w' and 2w' + 1, w' = wave % (KC / 64) (with KC = 128 waves 2
+    // and 3 repeat waves 0 and 1 and write nothing).
 #pragma unroll
     for (int tok = 0; tok < TT; ++tok) {
+        float ss[2];
 #pragma unroll
-        for (int c = 0; c < kNV; ++c) {
+        for (int h = 0; h < 2; ++h) {
             float xa[8], ra[8];
-            unpack8_f32(px[tok][c], xa);
-            if constexpr (RESID) unpack8_f32(pr[tok][c], ra);
-            float ss = 0.f;
+            unpack8_f32(sx[tok][h], xa);
+            if constexpr (RESID) unpack8_f32(sr[tok][h], ra);
+            ss[h] = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float v = RESID ? xa[e] + ra[e] : xa[e];
-                ss = fmaf(v, v, ss);
+                ss[h] = fmaf(v, v, ss[h]);
             }
-            ss = wave_sum(ss);
-            if (lane == 0) red[tok][wave + kWaves * c] = ss;
+#pragma unroll
+            for (int m = 16; m > 0; m >>= 1) ss[h] += __shfl_xor(ss[h], m, 64);
         }
+        const float wsum = ss[0] + ss[1];
+        if ((lane & 31) == 0 && wave < KC / 64) red[tok][2 * wave + (lane >> 5)] = wsum;
     }
     __syncthreads();
     const bool writer = blockIdx.x == 0 && t < KC;
