@@ -803,17 +803,23 @@ hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
 // dots outweigh its fixed costs. Its 16-row workgroups cover a matrix with
 // N/16 workgroups, and each wave load spans 16 rows x 64 B, so at small N or
 // few tokens the vector kernels (more workgroups, 1 KiB row loads) are
-// faster. Measured on MI355X over the MLA shapes (576, 1536, 4096 rows; K =
-// 1024 .. 8192; T = 1 .. 16): the matrix cores win from T = 4 at N >= 2048,
-// from T = 9 at N >= 1024, and from T = 2 at K = 8192. The rule looks at one
-// matrix's (or one group's) rows, so a grouped launch takes the path of a
-// single GEMV on each group.
+// faster, and the longer the rows the more tokens it takes for the matrix
+// cores to win. Measured on MI355X (graph replay over 512 MB of rotated
+// weights; N = 576 .. 8192, K = 1024 .. 4096, T = 2 .. 16) the crossover is
+//   K = 1024: T >= 3 at N >= 2048, T >= 5 at N >= 1024;
+//   K = 2048: T >= 3 at N >= 4096, T >= 5 at N >= 1536;
+//   K = 4096: T >= 3 at N >= 4096, T >= 9 at N >= 1536;
+//   K = 8192: T >= 2.
+// The rule looks at one matrix's (or one group's) rows, so a grouped launch
+// takes the path of a single GEMV on each group.
 // The matrix-core kernel reads the T activation rows through one buffer
 // resource, whose byte extent must fit 31 bits.
 bool use_mfma(int T, int K, int N, int64_t xstride) {
     if (T < 2 || ((int64_t)(T - 1) * xstride + K) * 2 > INT32_MAX) return false;
     if (K > 4096) return true;
-    return (T >= 4 && N >= 2048) || (T > 8 && N >= 1024);
+    if (K <= 1024) return (T >= 3 && N >= 2048) || (T >= 5 && N >= 1024);
+    if (K <= 2048) return (T >= 3 && N >= 4096) || (T >= 5 && N >= 1536);
+    return (T >= 3 && N >= 4096) || (T >= 9 && N >= 1536);
 }
 
 // The matrix-core path (T >= 2 on the tile shapes): NW waves of 512 k each,

@@ -17,7 +17,7 @@ from tests.gpu_util import announce, assert_close, dev_bf16, dev_u8, host_bits
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("N,K,T", [(32768, 1024, 1), (4096, 1024, 3), (130, 1024, 16),
+@pytest.mark.parametrize("N,K,T", [(32768, 1024, 1), (1040, 1024, 3), (130, 1024, 16),
                                    (4096, 8192, 1), (4096, 8192, 2), (4096, 8192, 5), (300, 8192, 16),
                                    (4096, 4096, 16), (1000, 2048, 11)])
 def test_fp8_tile_engine_shapes(device, N, K, T):
@@ -68,12 +68,13 @@ def test_fp8_swiglu_gemv_engine_k(device, N, K, T):
                  f"fp8 swiglu N={N} K={K} T={T}")
 
 
-# Shapes on the matrix-core path (T >= 4 at N >= 2048, T > 8 at N >= 1024,
+# Shapes on the matrix-core path (T >= 3 at N >= 4096, or N >= 2048 at
+# K = 1024; T >= 5 at N >= 1536, or N >= 1024 at K = 1024, T >= 9 at K = 4096;
 # T >= 2 at K = 8192) next to the vector path at the same K: every K of the
 # tile set (2, 4, 8 and 16 waves per workgroup), a last 16-row block that is
 # partly past N, and K = 8192 with two matrices (two passes per wave).
-@pytest.mark.parametrize("N,K,T", [(2048, 1024, 8), (2050, 2048, 5), (4096, 2048, 4), (1100, 4096, 9),
-                                   (2048, 4096, 3), (4096, 8192, 16), (64, 8192, 2)])
+@pytest.mark.parametrize("N,K,T", [(2048, 1024, 8), (2050, 2048, 5), (4096, 2048, 4), (1540, 4096, 9),
+                                   (4100, 4096, 3), (4096, 8192, 16), (64, 8192, 2)])
 def test_fp8_matrix_core_path(device, N, K, T):
     announce(f"fp8_e4m3_gemv matrix-core path N={N} K={K} T={T}")
     w, s = synth.fp8_weight(16000 + N + K, N, K)
@@ -126,7 +127,7 @@ def test_fp8_matrix_core_groups_straddle_scale_tiles(device):
     """Groups of 2056 rows: the second group starts 8 rows into a 16-row
     block, so its blocks straddle 128-row scale tiles; each group's bits equal
     a single GEMV on its slice (both on the matrix cores)."""
-    G, N, K, T = 2, 2056, 2048, 4
+    G, N, K, T = 2, 2056, 2048, 5
     announce(f"fp8_e4m3_gemv_grouped matrix-core G={G} N={N} K={K} T={T}")
     w, s = synth.fp8_weight(16200, G * N, K)
     x = synth.normal_bf16(16201, (T, G, K))
@@ -139,7 +140,7 @@ def test_fp8_matrix_core_groups_straddle_scale_tiles(device):
     assert np.array_equal(host_bits(y0).reshape(T, N), got[:, 0])
 
 
-@pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (2048, 4096, 8), (2048, 8192, 3), (1024, 2048, 12),
+@pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (2048, 4096, 9), (2048, 8192, 3), (1536, 2048, 12),
                                    (8192, 2048, 8), (8200, 2048, 9)])
 def test_fp8_swiglu_matrix_core(device, N, K, T):
     """The fused SwiGLU on the matrix cores (K = 8192 runs two passes per
@@ -164,7 +165,7 @@ def test_fp8_swiglu_matrix_core(device, N, K, T):
 def test_fp8_multi_matrix_core(device):
     """Two matrices on the matrix cores in one launch: each output has the bits
     of the single launch on that matrix."""
-    shapes, K, T = [4096, 2048], 4096, 8
+    shapes, K, T = [4096, 2048], 4096, 9
     announce(f"fp8_e4m3_gemv_multi matrix-core N={shapes} K={K} T={T}")
     mats, dmats = [], []
     for i, N in enumerate(shapes):
