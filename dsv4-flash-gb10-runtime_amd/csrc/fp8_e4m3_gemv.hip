@@ -15,6 +15,7 @@
 // N need not be a multiple of 128 (ceil(N/128) scale rows), unlike reference
 // kernel/fp8-dense/fp8_e4m3_gemv.cu:148-154.
 
+#include <algorithm>
 #include <cstdio>
 #include <initializer_list>
 
@@ -810,8 +811,12 @@ hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
 //   K = 2048: T >= 3 at N >= 4096, T >= 5 at N >= 1536;
 //   K = 4096: T >= 3 at N >= 4096, T >= 9 at N >= 1536;
 //   K = 8192: T >= 2.
-// The rule looks at one matrix's (or one group's) rows, so a grouped launch
-// takes the path of a single GEMV on each group.
+// The fused SwiGLU and the RMSNorm-folded GEMV apply it to one matrix's
+// rows, so their GEMVs keep the bits of fp8_e4m3_gemv on the same rows. A
+// grouped launch applies it to the rows of all its groups, which is what sets
+// its workgroup count: 8 groups of 1024 x 4096 run on the matrix cores from
+// T = 3 (9.5 against 11.8 us; 13.5 against 31.7 us at T = 16), where a
+// single 1024-row GEMV stays on the vector kernels.
 // The matrix-core kernel reads the T activation rows through one buffer
 // resource, whose byte extent must fit 31 bits.
 bool use_mfma(int T, int K, int N, int64_t xstride) {
@@ -904,7 +909,8 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
 int launch(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
     if (tile_ok(a)) {
-        e = use_mfma(a.T, a.K, a.N, a.xstride) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
+        const int rows = (int)std::min<int64_t>((int64_t)a.N * G, INT32_MAX);
+        e = use_mfma(a.T, a.K, rows, a.xstride) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
                                      : launch_tile<1>(a, SwigluArgs{}, G, stream);
     } else {
         const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);

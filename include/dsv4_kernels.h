@@ -317,8 +317,10 @@ int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_f
  * with W [G*N, K] (scale rows (g*N+n)/128), x element (t, g, k) at
  * x + t*x_row_stride + g*x_group_stride + k, y element (t, g, n) at
  * y + t*y_row_stride + g*y_group_stride + n. The path rule of fp8_e4m3_gemv
- * applies to one group's N, so each group has the bits of fp8_e4m3_gemv on its
- * slice. Returns as fp8_e4m3_gemv, plus -6 for G < 1 or G > 65535. */
+ * applies to the rows of all groups (G*N), so a group has the bits of
+ * fp8_e4m3_gemv on its slice whenever that call takes the same path (always at
+ * T = 1; within fp32 rounding of the sums otherwise). Returns as
+ * fp8_e4m3_gemv, plus -6 for G < 1 or G > 65535. */
 int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_group_stride,
                           const uint8_t* W_fp8, const uint8_t* W_scale, int G, int K, int N, int T,
                           int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
