@@ -61,29 +61,71 @@ STAGE_B_EXPERT_BYTES = O * H // 2 + O * H // 32         # 4,456,448 B (W2)
 MALL_DEFEAT_BYTES = 512 << 20                           # rotate weight copies over >= 2x the 256 MB MALL
 
 
+VERBOSE = False
+
+
 def log(msg: str) -> None:
-    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+    """Progress on stderr with --verbose only: the driver keeps the last
+    2,000 characters of stdout + stderr, which belong to the JSON line."""
+    if VERBOSE:
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def topk_ids(logits: np.ndarray, k: int = TOPK) -> np.ndarray:
     return np.argsort(-logits.astype(np.float64), axis=1, kind="stable")[:, :k]
 
 
-def profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` ("name@T<tokens>") from the rocprofv3
-    counter summaries in profiles/*.md (lines `TRAFFIC <kernel>@T<tokens>
-    <bytes>`); returns (bytes, file) or (None, None)."""
+CSRC = os.path.join(PKG, "csrc")
+
+
+def source_sha(name: str) -> str:
+    """First 12 hex digits of the SHA-256 of a kernel source file (csrc/)."""
+    import hashlib
+    with open(os.path.join(CSRC, name), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:12]
+
+
+def _profile_lines(tag: str):
+    """Machine-readable lines of profiles/*.md: `SOURCE <file> <sha12>` (the
+    kernel sources the profile was taken from) and `<tag> <key> <value> ...
+    <file>[,<file>...]`. Yields (key, fields, profile file, stale) where stale
+    says that one of the line's source files changed since the profile."""
     d = os.path.join(REPO, "profiles")
     if not os.path.isdir(d):
-        return None, None
+        return
     for name in sorted(os.listdir(d)):
         if not name.endswith(".md"):
             continue
         with open(os.path.join(d, name)) as f:
-            for line in f:
-                parts = line.split()
-                if len(parts) == 3 and parts[0] == "TRAFFIC" and parts[1] == kernel:
-                    return int(parts[2]), "profiles/" + name
+            lines = [ln.split() for ln in f]
+        shas = {p[1]: p[2] for p in lines if len(p) == 3 and p[0] == "SOURCE"}
+        for p in lines:
+            if len(p) >= 4 and p[0] == tag:
+                files = p[-1].split(",")
+                stale = any(fn not in shas or not os.path.exists(os.path.join(CSRC, fn))
+                            or source_sha(fn) != shas[fn] for fn in files)
+                yield p[1], p[2:-1], "profiles/" + name, stale
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` ("name@T<tokens>") from the rocprofv3
+    counter summaries in profiles/*.md (lines `TRAFFIC <kernel>@T<tokens>
+    <bytes> <source files>`); returns (bytes, file), or (None, None) when no
+    profile has the kernel or its sources changed since the profile."""
+    for key, fields, src, stale in _profile_lines("TRAFFIC"):
+        if key == kernel and not stale:
+            return int(fields[0]), src
+    return None, None
+
+
+def profiled_duration(kernel: str):
+    """rocprofv3 kernel-trace average duration (µs) of `kernel`'s launches in
+    the bench's own roofline timing (lines `DURATION <kernel>@T<tokens> <µs>
+    <dispatches> <source files>` of profiles/*.md); (µs, file) or (None, None)
+    when absent or stale."""
+    for key, fields, src, stale in _profile_lines("DURATION"):
+        if key == kernel and not stale:
+            return float(fields[0]), src
     return None, None
 
 
@@ -175,9 +217,9 @@ def moe_layer_case(torch, dev, layers, T: int, steps: int, warmup: int, seed: in
     for st in sts:
         st.down(yo)
     torch.cuda.synchronize()
-    a_gate_us = tm.graph_us_per_call(lambda: [st.gate_swiglu(x, logits[i]) for i, st in enumerate(sts)], R, reps=2)
+    a_gate_us = tm.graph_us_per_call(lambda: [st.gate_swiglu(x, logits[i]) for i, st in enumerate(sts)], R, reps=4)
     a_us = tm.graph_us_per_call(lambda: [st.swiglu(x) for st in sts], R, reps=2)
-    b_us = tm.graph_us_per_call(lambda: [st.down(yo) for st in sts], R, reps=2)
+    b_us = tm.graph_us_per_call(lambda: [st.down(yo) for st in sts], R, reps=4)
     a_bytes = float(np.mean(uniq[:R] * STAGE_A_EXPERT_BYTES + T * K * 2 + T * E * 4))
     b_bytes = float(np.mean(uniq[:R] * STAGE_B_EXPERT_BYTES + T * O * 2))
     out["stage_us"] = {"gate_swiglu_A": round(a_gate_us, 3), "swiglu_A_tables_given": round(a_us, 3),
@@ -640,10 +682,21 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def cpu_quota_cores():
+    """CPUs granted by the cgroup v2 quota (cpu.max), or None without one."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, p = f.read().split()[:2]
+        return None if q == "max" else round(int(q) / int(p), 2)
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(torch, layer, x, logits_h, T: int, step_bytes: float) -> dict:
     """The CPU oracle (the reference's CPU path: unpack + E8M0 -> bf16 dequant,
-    fp32 matmul, bf16 casts) on one step of the headline workload, on the
-    host's cores, and the same layer on weights dequantised beforehand."""
+    fp32 matmul, bf16 casts) on one step of the headline workload, on every
+    core of the host (os.cpu_count() BLAS threads), and the same layer on
+    weights dequantised beforehand."""
     from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle import mx
@@ -660,7 +713,7 @@ def cpu_baseline(torch, layer, x, logits_h, T: int, step_bytes: float) -> dict:
     xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
     for e in np.unique(ids_t):
         expert(int(e))
-    threads = min(os.cpu_count() or 1, 16)
+    threads = os.cpu_count() or 1
     with threadpool_limits(limits=threads):
         blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
         log(f"cpu baseline: oracle moe layer, {threads} BLAS threads")
@@ -688,10 +741,11 @@ def cpu_baseline(torch, layer, x, logits_h, T: int, step_bytes: float) -> dict:
         "matmul_only_us_per_layer": round(mm_s * 1e6, 1),
         "cores": int(blas[0]) if blas else threads,
         "kind": "port",
-        "sample": (f"{n_calls} call(s) of the numpy oracle moe_layer (unpack + E8M0 scale -> bf16 dequant, "
-                   f"fp32 matmul, bf16 casts) on step 0: T={T}, {len(np.unique(ids_t))} routed experts of "
-                   f"layer 0; host {cpu_model()}, nproc {os.cpu_count()}; matmul_only_us_per_layer: {n_mm} "
-                   f"call(s) of the same layer on weights dequantised to fp32 beforehand"),
+        "nproc": os.cpu_count(),
+        "cpu_quota_cores": cpu_quota_cores(),
+        "cpu_model": cpu_model(),
+        "sample": (f"{n_calls} oracle moe_layer call(s), T={T}, {len(np.unique(ids_t))} experts "
+                   f"(dequant+fp32 matmul); matmul_only: {n_mm} call(s) on pre-dequantised weights"),
     }
 
 
@@ -756,7 +810,10 @@ def main() -> int:
                     help="skip the other configurations (config 3 at T=4/16, dispatch, config 4)")
     ap.add_argument("--c4-layers", type=int, default=43, help="layers of the config-4 sweep")
     ap.add_argument("--counters", action="store_true", help="short fixed sequence for rocprofv3 --pmc")
+    ap.add_argument("--verbose", action="store_true", help="progress lines on stderr")
     args = ap.parse_args()
+    global VERBOSE
+    VERBOSE = args.verbose or args.counters
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(the routed MoE would shard by experts, or by the ff dimension with one all-reduce "
@@ -842,10 +899,17 @@ def main() -> int:
     b_traffic, b_src = profiled_traffic(f"{b_kernel}@T{T}")
 
     def roof(kernel, desc, us, nbytes, traffic, src):
+        # achieved / frac: this run's HIP-event average per launch; rocprof_*:
+        # the kernel-trace average of the same timing launches in
+        # profiles/ (null when the kernel's sources changed since)
+        rp_us, rp_src = profiled_duration(f"{kernel}@T{T}")
         return {"kernel": f"{kernel} ({desc})", "bound": "hbm", "achieved": round(gbs(nbytes, us), 2),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs(nbytes, us) / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "traffic_source": src, "algorithmic_bytes_per_launch": int(round(nbytes)),
-                "avg_launch_us": round(us, 3)}
+                "avg_launch_us": round(us, 3),
+                "rocprof_avg_us": rp_us,
+                "rocprof_frac": round(gbs(nbytes, rp_us) / HBM_PEAK_GBS, 4) if rp_us else None,
+                "rocprof_source": rp_src}
 
     result = {
         "metric": METRIC,
@@ -879,9 +943,8 @@ def main() -> int:
         "stage_b_roofline": roof(b_kernel, "stage B: W2 MXFP4 GEMV + weighted combine", b_us, b_bytes,
                                  b_traffic, b_src),
         "cpu_baseline": cpu,
-        "configs": configs,
         "kernels": kernels,
-        "bench_seconds": round(time.perf_counter() - t_start, 1),
+        "configs": configs,
     }
     # the measured device-copy ceiling (torch's copy over 1 GiB, read + write)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -895,8 +958,64 @@ def main() -> int:
     result["read_floor"] = read_floor_case(torch, dev, {
         "stage_A": (a_bytes, a_us), "stage_B": (b_bytes, b_us),
         "layer_one_pass": (a_bytes + b_bytes, result["moe_layer_us"])})
-    print(json.dumps(result), flush=True)
+    result["bench_seconds"] = round(time.perf_counter() - t_start, 1)
+    # last key: every configuration in a few characters, so that it falls in
+    # the tail of the output that a driver keeps
+    result["summary"] = summary(result)
+    print(json.dumps(result, separators=(",", ":")), flush=True)
     return 0
+
+
+def summary(r: dict) -> dict:
+    """[µs, fraction of 8 TB/s (algorithmic bytes / time), kernel time over
+    the read floor for the same bytes] per configuration and kernel; prefill
+    adds the fraction of the bf16 MFMA peak; stage A/B add the rocprof average
+    from profiles/ (µs) and the fraction it gives."""
+    def r3(v):
+        return None if v is None else round(v, 3)
+
+    rf = r.get("read_floor", {})
+    s = {"cols": "us,frac_hbm,over_floor"}
+    s["cfg3_T%d" % r["config"]["tokens"]] = [r3(r["moe_layer_us"]), r3(r["hbm_frac_of_peak"]),
+                                              r3(rf.get("layer_one_pass", {}).get("kernel_over_floor"))]
+    for tag, key in (("A", "roofline"), ("B", "stage_b_roofline")):
+        ro = r[key]
+        floor = rf.get("stage_" + tag, {}).get("kernel_over_floor")
+        s["stage" + tag] = [r3(ro["avg_launch_us"]), r3(ro["frac"]), r3(floor), ro["rocprof_avg_us"],
+                            r3(ro["rocprof_frac"])]
+    c = r.get("configs") or {}
+    for k in ("cfg3_T1", "cfg3_T4", "cfg3_T16"):
+        if k in c:
+            s[k] = [r3(c[k]["moe_layer_us"]), r3(c[k]["hbm_frac_of_peak"])]
+    if "routed_dispatch_T1" in c:
+        s["dispatch_T1"] = [r3(c["routed_dispatch_T1"]["us"]), r3(c["routed_dispatch_T1"]["hbm_frac_of_peak"])]
+    if "cfg4_decode" in c:
+        d = c["cfg4_decode"]
+        s["cfg4_decode_layer"] = [r3(d["us_per_layer"]), r3(d["hbm_frac_of_peak"])]
+    if "cfg4_prefill" in c:
+        p = c["cfg4_prefill"]
+        s["cfg4_prefill_layer"] = [round(p["us_per_layer"], 1), r3(p["hbm_frac_of_peak"]),
+                                   r3(p.get("read_floor", {}).get("layer_bytes", {}).get("kernel_over_floor")),
+                                   r3(p["mfma_frac_of_bf16_peak"])]
+    short = {"mxfp4_gemv_m1 2048x4096": "cfg0_mxfp4",
+             "fp8_e4m3_gemv_multi wq_a 1024x4096 + wkv 512x4096 T=1": "fp8_multi_wqa_wkv",
+             "fp8_e4m3_gemv_grouped wo_a 8x1024x4096 T=1": "fp8_grouped_wo_a",
+             "fp8_e4m3_swiglu_gemv shared expert 2x2048x4096 T=1": "fp8_swiglu_shared",
+             "fp8_e4m3_rmsnorm_gemv residual+norm+wq_a 1536x4096 T=1": "fp8_rmsnorm_wqa",
+             "router_logits bf16 256x4096 T=1": "router_gemv"}
+    for name, e in (r.get("kernels") or {}).items():
+        m = re.match(r"fp8_e4m3_gemv (?:(wq_b|wo_b) )?(\d+)x(\d+) T=(\d+)$", name)
+        if m:
+            key = f"fp8_{m.group(2)}x{m.group(3)}_T{m.group(4)}"
+        else:
+            m = re.match(r"rmsnorm_fuse_residual_add T=(\d+)x\d+$", name)
+            key = f"cfg1_rmsnorm_T{m.group(1)}" if m else short.get(name)
+        if key:
+            s[key] = [r3(e["us"]), r3(e["frac_of_peak"]), r3(e.get("kernel_over_floor"))]
+    if r.get("cpu_baseline"):
+        cb = r["cpu_baseline"]
+        s["cpu_baseline"] = [cb["us_per_layer"], cb["cores"]]
+    return s
 
 
 if __name__ == "__main__":

@@ -380,11 +380,16 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
             sr[1][b] = sw.s3 + (gn / kTile) * a.srow;
         }
     }
-    f32x4 acc[MAT][R];
+    // One accumulator per pass: each 512-k block's sum starts from zero, so
+    // a wave of several passes produces exactly the partials that one wave
+    // per block would (the blocks are added in k order at the end).
+    f32x4 acc[PASSES][MAT][R];
 #pragma unroll
-    for (int m = 0; m < MAT; ++m)
+    for (int p = 0; p < PASSES; ++p)
 #pragma unroll
-        for (int b = 0; b < R; ++b) acc[m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < MAT; ++m)
+#pragma unroll
+            for (int b = 0; b < R; ++b) acc[p][m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int k0 = (wave * PASSES + p) * kMmaK;
@@ -434,16 +439,18 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
                     }
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        acc[m][b][i] = fmaf(ts[i], e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu), acc[m][b][i]);
+                        acc[p][m][b][i] = fmaf(ts[i], e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu), acc[p][m][b][i]);
                 }
             }
     }
 #pragma unroll
-    for (int m = 0; m < MAT; ++m)
+    for (int p = 0; p < PASSES; ++p)
 #pragma unroll
-        for (int b = 0; b < R; ++b)
+        for (int m = 0; m < MAT; ++m)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) part[wave][m][16 * b + 4 * g + i][r] = acc[m][b][i];
+            for (int b = 0; b < R; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) part[wave * PASSES + p][m][16 * b + 4 * g + i][r] = acc[p][m][b][i];
     __syncthreads();
     for (int o = t; o < 256 * R; o += 64 * NW) {
         const int tok = o / (16 * R);
@@ -454,7 +461,7 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
         for (int m = 0; m < MAT; ++m) {
             sum[m] = 0.f;
 #pragma unroll
-            for (int w2 = 0; w2 < NW; ++w2) sum[m] += part[w2][m][row][tok];
+            for (int w2 = 0; w2 < NW * PASSES; ++w2) sum[m] += part[w2][m][row][tok];
         }
         uint16_t out;
         if constexpr (MAT == 2) {
@@ -472,7 +479,7 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
 // One matrix, or G row groups of one matrix (blockIdx.y); grid.x = ceil(N/(16R)).
 template <int NW, int PASSES, int MAT, int R>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_mfma_kernel(const Fp8Args a, const SwigluArgs sw) {
-    __shared__ float part[NW][MAT][16 * R][16];
+    __shared__ float part[NW * PASSES][MAT][16 * R][16];
     fp8_mfma_body<NW, PASSES, MAT, R>(a, sw, group_view(a), blockIdx.x, part);
 }
 
@@ -1171,9 +1178,9 @@ extern "C" int fp8_e4m3_rmsnorm_gemv(const dsv4_bf16_t* x, const dsv4_bf16_t* re
 #undef DSV4_NG
         e = hipGetLastError();
     } else {
-        // Where fp8_e4m3_gemv takes the matrix cores (here T = 4, N >= 2048):
-        // the norm in one workgroup, then that GEMV on x_norm (so y keeps its
-        // bits).
+        // Where fp8_e4m3_gemv takes the matrix cores (use_mfma; with T <= 4
+        // and K in {2048, 4096} that is T >= 3 with N >= 4096): the norm in
+        // one workgroup, then that GEMV on x_norm (so y keeps its bits).
 #define DSV4_NO(KCV, RES) \
     hipLaunchKernelGGL((fp8_norm_gemv_tile_kernel<4, 4, KCV, RES, false>), dim3(1), dim3(256), 0, stream, a, nm)
         if (residual) { if (KC == 256) DSV4_NO(256, true); else DSV4_NO(128, true); }

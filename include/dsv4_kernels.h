@@ -151,7 +151,10 @@ int mxfp4_moe_grouped_gemv(const dsv4_bf16_t* x,
  * (the same bits) and return codes as mxfp4_moe_grouped_gemv, plus -8 when
  * mxfp4_moe_workspace_bytes(T, topk, n_experts, hidden) exceeds 4 MiB
  * (e.g. T*topk*hidden*2 above about 4.1 million bytes) and -9 when the device
- * array cannot be located. */
+ * array cannot be located. The first call on each device looks the array's
+ * address up (hipGetSymbolAddress, a runtime query, no stream work): make that
+ * first call outside graph capture; captured calls after it record only the
+ * kernel launches. */
 int mxfp4_moe_grouped_gemv_noalloc(const dsv4_bf16_t* x,
                                    const uint8_t* W1_packed, const uint8_t* W3_packed,
                                    const uint8_t* W2_packed,

@@ -179,3 +179,29 @@ def test_fp8_multi_matrix_core(device):
         got = host_bits(y).reshape(T, N)
         assert np.array_equal(got, host_bits(fp8b.fp8_e4m3_gemv(tw, ts, xd)).reshape(T, N))
         assert_close(got, mx.fp8_gemv(x, w, s), f"multi matrix-core N={N}")
+
+
+@pytest.mark.parametrize("N,K,T", [(2048, 8192, 2), (2048, 8192, 3), (4096, 4096, 4), (2048, 1024, 4),
+                                   (8192, 2048, 8)])
+def test_fp8_swiglu_matrix_core_keeps_gemv_bits(device, N, K, T):
+    """Gate and up of the fused SwiGLU on the matrix cores are exactly the
+    bits of fp8_e4m3_gemv on each matrix (K = 8192 included, where a wave
+    takes two 512-k blocks). Inputs make the SiLU exact in fp32: non-negative
+    weights and activations give gate sums >= 17, where exp(-g) < 2^-24 and
+    1 + exp(-g) rounds to 1, so act = bf16(bf16(gate) * bf16(up)) with an
+    exact fp32 product, and any change in either sum's bits shows (0 ulp)."""
+    announce(f"fp8_e4m3_swiglu_gemv bit equality N={N} K={K} T={T}")
+    w1, s1 = synth.fp8_weight(16900 + N + K, N, K)
+    w3, s3 = synth.fp8_weight(17000 + N + K, N, K)
+    w1 = (w1 & 0x7F).astype(np.uint8)         # |W1| (no 0xFF codes, so no NaN appears)
+    x = (synth.normal_bf16(17100 + T, (T, K)) & 0x7FFF).astype(np.uint16)
+    x = mx.bf16_round(4 * mx.bf16_to_f32(x))
+    t1, u1, t3, u3 = dev_u8(w1, device), dev_u8(s1, device), dev_u8(w3, device), dev_u8(s3, device)
+    xd = dev_bf16(x, device)
+    act = host_bits(fp8b.fp8_e4m3_swiglu_gemv(t1, u1, t3, u3, xd, 0.0, False)).reshape(T, N)
+    gate = host_bits(fp8b.fp8_e4m3_gemv(t1, u1, xd)).reshape(T, N)
+    up = host_bits(fp8b.fp8_e4m3_gemv(t3, u3, xd)).reshape(T, N)
+    g = mx.bf16_to_f32(gate)
+    assert g.min() >= 17.0, f"gate sums must be >= 17 for an exact SiLU, min {g.min()}"
+    ref = mx.bf16_round((g * mx.bf16_to_f32(up)).astype(np.float32))
+    assert np.array_equal(act, ref), f"{int(np.sum(act != ref))} outputs differ from bf16(gate * up)"

@@ -566,16 +566,37 @@ def test_moe_indexed_config_dims(device, T):
 
 
 def test_moe_indexed_equals_packed_dropin(device):
-    """Full-size T=16: each token's row equals the drop-in call on its packed experts."""
+    """Full-size T=16 (configuration 3): three tokens' rows against the
+    oracle directly, and each token's row equal to the drop-in call on its
+    packed experts."""
     from runtime import moe
 
     E, K, H, O, T = 256, 4096, 2048, 4096, 16
-    announce(f"mxfp4_moe_grouped_gemv vs mxfp4_grouped_gemv_topk T={T}")
+    announce(f"mxfp4_moe_grouped_gemv vs oracle and mxfp4_grouped_gemv_topk T={T}")
     weights = moe.make_moe_weights(9500, E, K, H, O, device)
     layer = moe.RoutedMoELayer(weights, topk=8, max_tokens=16)
-    x = dev_bf16(synth.normal_bf16(9600, (T, K)), device)
-    logits = dev_f32(synth.gating_logits(9601, T, E), device)
+    xh = synth.normal_bf16(9600, (T, K))
+    x = dev_bf16(xh, device)
+    lh = synth.gating_logits(9601, T, E)
+    logits = dev_f32(lh, device)
     out = host_bits(layer.forward(x, logits=logits))
+    ids_h = layer.ids[:T].cpu().numpy()
+    w_h = layer.weights[:T].cpu().numpy()
+    rids, _ = mx.route_sigmoid_topk(lh, 8)
+    assert np.array_equal(ids_h, rids)
+    cache = {}
+
+    def fn(e):
+        if e not in cache:
+            cache[e] = tuple((m["packed"][e].cpu().numpy(), m["scale"][e].cpu().numpy())
+                             for m in (weights.W1, weights.W3, weights.W2))
+        return cache[e]
+
+    sel = [0, 7, 15]
+    ref = mx.moe_layer(xh[sel], fn, ids_h[sel], w_h[sel], O)
+    for i, t in enumerate(sel):
+        assert_close(out[t], ref[i], f"T=16 token {t} vs the oracle")
+    cache.clear()
     ids = layer.ids[:T].long()
     for t in range(T):
         sel = ids[t]

@@ -209,6 +209,57 @@ def test_chained_decode_three_layers(device):
     torch.cuda.empty_cache()
 
 
+def test_chained_decode_graph_replays_match_eager(device):
+    """Config 4's timed form: three configuration-3 layers chained on the ids
+    path (forward(ids=...): stage A forms the slots from the caller's ids,
+    two launches per layer), captured in one HIP graph, as bench.py times the
+    43-layer sweep (the reference engine's decode loop,
+    kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu:742-845, captured and
+    replayed as in graph.cu:118,187). Every replay, with eager work of other
+    routings and inputs between replays, must give the eager chain's bits,
+    and the last layer's output must match the oracle's own three-layer
+    chain."""
+    L = 3
+    layers = [moe.make_moe_weights(12700 + 100 * l, E3, K3, H3, O3, device) for l in range(L)]
+    mods = [moe.RoutedMoELayer(w, topk=8, max_tokens=1, check=False) for w in layers]
+    routing = [synth.zipf_routing(12800, 2, E3, 8, 1.1, layer=l) for l in range(L)]
+    ids_d = [torch.from_numpy(r[0]).to(device) for r in routing]
+    w_d = [dev_f32(r[1], device) for r in routing]
+    x0 = synth.normal_bf16(12801, (1, K3))
+    x1 = synth.normal_bf16(12802, (1, K3))
+    xin = dev_bf16(x0, device)
+
+    def chain(step):
+        x = xin
+        for l in range(L):
+            x = mods[l].forward(x, ids=ids_d[l][step:step + 1], weights=w_d[l][step:step + 1])
+        return x
+
+    announce(f"graph-captured chained decode: {L} layers, ids path, K={K3}")
+    out = chain(0)
+    eager = host_bits(out).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        captured_out = chain(0)
+    assert captured_out.data_ptr() == out.data_ptr()
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        assert np.array_equal(host_bits(out), eager), f"replay {rep} differs from the eager chain"
+        # eager work between replays: the other routing step on another input
+        xin.copy_(dev_bf16(x1, device))
+        chain(1)
+        torch.cuda.synchronize()
+        xin.copy_(dev_bf16(x0, device))
+    x_ref = x0
+    for l in range(L):
+        ids, wt = routing[l][0][:1], routing[l][1][:1]
+        x_ref = mx.moe_layer(x_ref, _host_expert_fn(layers[l]), ids, wt, O3)
+    assert_close(eager, x_ref, "graph-captured three-layer chain vs the oracle's chain")
+    del g, mods, layers
+    torch.cuda.empty_cache()
+
+
 # ------------------------------------------- the reference engine's router --
 
 @pytest.mark.parametrize("T,E,K", [(1, 256, 4096), (5, 200, 1000), (16, 256, 4096)])

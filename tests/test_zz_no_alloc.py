@@ -52,3 +52,36 @@ def test_noalloc_matches_workspace_entry_two_calls(device):
     assert _noalloc(x, w, ids, wt, out) == -8
     del w
     torch.cuda.empty_cache()
+
+
+def test_noalloc_captured_in_a_graph_replays_match_eager(device):
+    """The entry's use under HIP graph capture: after one eager call on the
+    device (which looks up the array's address), a captured call replays to
+    the eager bits, with eager calls of both entries on other inputs between
+    the replays (they share the array; one stream orders them)."""
+    E, K, H, O, topk, T = 32, 4096, 2048, 4096, 8, 1
+    w = moe.make_moe_weights(14400, E, K, H, O, device)
+    announce(f"mxfp4_moe_grouped_gemv_noalloc under graph capture: T={T} E={E} K={K}")
+    x = dev_bf16(synth.normal_bf16(14500, (T, K)), device)
+    ids, wt = synth.zipf_routing(14600, 2, E, topk, 1.1)
+    idd, wd = torch.from_numpy(ids).to(device), dev_f32(wt, device)
+    out = torch.empty(T, O, dtype=torch.bfloat16, device=device)
+    assert _noalloc(x, w, idd[:1], wd[:1], out) == 0
+    eager = host_bits(out).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        assert _noalloc(x, w, idd[:1], wd[:1], out) == 0
+    x2 = dev_bf16(synth.normal_bf16(14501, (4, K)), device)
+    ids2, wt2 = synth.zipf_routing(14601, 4, E, topk, 1.1)
+    id2, wd2 = torch.from_numpy(ids2).to(device), dev_f32(wt2, device)
+    out2 = torch.empty(4, O, dtype=torch.bfloat16, device=device)
+    for rep in range(3):
+        out.zero_()
+        g.replay()
+        assert np.array_equal(host_bits(out), eager), f"replay {rep} differs from the eager call"
+        assert _noalloc(x2, w, id2, wd2, out2) == 0
+        gb.mxfp4_moe_grouped_gemv(x, w.W1, w.W3, w.W2, idd[1:], wd[1:])
+        torch.cuda.synchronize()
+    assert np.array_equal(host_bits(out2), host_bits(gb.mxfp4_moe_grouped_gemv(x2, w.W1, w.W3, w.W2, id2, wd2)))
+    del g, w
+    torch.cuda.empty_cache()
