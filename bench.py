@@ -463,6 +463,19 @@ def dense_kernels(torch, dev, cpu: bool, counters: bool = False) -> dict:
             out[f"fp8_e4m3_gemv {N}x{Kf} T={T}"] = entry(us, wbytes + T * (2 * Kf + 2 * N),
                                                           cpu_us(lambda: mx.fp8_gemv(xh, w, ws)))
         del W, WS
+    # Rows longer than the tile set (K up to the reference's 16384 cap) with
+    # several tokens: each weight byte is read once for all tokens.
+    for (N, Kf) in ((2048, 6144), (1024, 12288)):
+        w, ws = synth.fp8_weight(1502 + N + Kf, N, Kf)
+        wbytes = N * Kf + ws.size
+        W, nW = copies(u8(w), wbytes)
+        WS = rep(u8(ws), nW)
+        T = 8
+        xdt = bf(synth.normal_bf16(2102 + Kf, (T, Kf)))
+        y = torch.empty((T, N), dtype=torch.bfloat16, device=dev)
+        us = time_launches(lambda i: fp8b.fp8_e4m3_gemv(W[i], WS[i], xdt, out=y), nW)
+        out[f"fp8_e4m3_gemv {N}x{Kf} T={T}"] = entry(us, wbytes + T * (2 * Kf + 2 * N), None)
+        del W, WS
 
     # The engine's MLA shapes (kernel/cpp-engine-mxfp4/dsv4_engine_mxfp4_wire.cu):
     # wq_a 1024x4096 and wkv 512x4096 on one activation (one multi launch

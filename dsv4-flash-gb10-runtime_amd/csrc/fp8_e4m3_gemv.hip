@@ -72,8 +72,15 @@ __device__ __forceinline__ u32x4 load_w16(const uint8_t* p) {
 // grid = ceil(N / (kWaves*kRows)), block = 64*kWaves. A row is walked in
 // segments of NC*1024 bytes (NC 16-byte chunks per lane, NC <= 4). With one
 // segment (K <= 4096) the rows stay in registers across all T tokens;
-// longer rows are re-streamed per token.
-template <int NC, bool ALIGNED>
+// longer rows are streamed once per group of kGenTok tokens (every token of
+// the group is accumulated from the segment in registers), so T <= 8 reads
+// each weight byte once. Each token's sum runs over the segments and chunks
+// in k order either way.
+// LONG selects the segmented body (NC = 4, K > 4096) at compile time, so the
+// one-segment kernels keep their smaller register budget.
+constexpr int kGenTok = 8;
+
+template <int NC, bool ALIGNED, bool LONG>
 __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -127,24 +134,38 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
                 acc[r] = fmaf(fp8_chunk_dot(wv[r][j], xp), sc[r][j], acc[r]);
         }
     };
-    if (nseg == 1) load_rows(0);
-    for (int t = 0; t < a.T; ++t) {
-        const uint16_t* xt = gv.x + (int64_t)t * a.xstride;
-        float acc[kRows];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
-        if (nseg == 1) {
-            accumulate(xt, 0, acc);
-        } else {
-            for (int seg = 0; seg < nseg; ++seg) {
-                load_rows(seg);
-                accumulate(xt, seg, acc);
-            }
-        }
+    auto store = [&](int t, float* acc) {
         wave_reduce_n<kRows>(acc, lane);
         const int r = reduced_index<kRows>(lane);
         if (reduced_owner<kRows>(lane) && n0 + r < a.N)
             gv.y[(int64_t)t * a.ystride + n0 + r] = f32_to_bf16_bits(acc[0]);
+    };
+    if (!LONG || nseg == 1) {
+        load_rows(0);
+        for (int t = 0; t < a.T; ++t) {
+            float acc[kRows];
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
+            accumulate(gv.x + (int64_t)t * a.xstride, 0, acc);
+            store(t, acc);
+        }
+        return;
+    }
+    for (int t0 = 0; t0 < a.T; t0 += kGenTok) {
+        float acc[kGenTok][kRows];
+#pragma unroll
+        for (int q = 0; q < kGenTok; ++q)
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) acc[q][r] = 0.f;
+        for (int seg = 0; seg < nseg; ++seg) {
+            load_rows(seg);
+#pragma unroll
+            for (int q = 0; q < kGenTok; ++q)
+                if (t0 + q < a.T) accumulate(gv.x + (int64_t)(t0 + q) * a.xstride, seg, acc[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < kGenTok; ++q)
+            if (t0 + q < a.T) store(t0 + q, acc[q]);
     }
 }
 
@@ -890,6 +911,37 @@ hipError_t launch_mfma(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
     return hipGetLastError();
 }
 
+// Rows longer than the tile set (K > 4096, K a multiple of 512, not 8192)
+// with several tokens: the matrix-core kernel with one wave per 512-k block
+// (PASSES = 1, up to 15 blocks) or per two blocks (PASSES = 2, an even count
+// up to 32, K <= 16384), so each weight byte is read once for all T tokens.
+// Operands as the tile kernels need them (16-byte aligned rows and
+// activations).
+int long_mfma_blocks(const Fp8Args& a) {
+    const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) && (a.T == 1 || a.xstride % 8 == 0) &&
+                    (a.xgroup % 8 == 0);
+    if (!al || a.T < 2 || a.K <= 4096 || a.K % kMmaK != 0 || tile_k(a.K) ||
+        ((int64_t)(a.T - 1) * a.xstride + a.K) * 2 > INT32_MAX)
+        return 0;
+    const int b = a.K / kMmaK;
+    return (b <= 15 || (b % 2 == 0 && b <= 32)) ? b : 0;
+}
+
+hipError_t launch_mfma_long(const Fp8Args& a, int blocks, int G, hipStream_t stream) {
+    const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)G);
+    const SwigluArgs sw{};
+#define DSV4_L1(NWV) case NWV: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<NWV, 1, 1, 1>), grid, dim3(64 * NWV), 0, stream, a, sw); break;
+#define DSV4_L2(NWV) case 2 * NWV: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<NWV, 2, 1, 1>), grid, dim3(64 * NWV), 0, stream, a, sw); break;
+    switch (blocks) {
+        DSV4_L1(9) DSV4_L1(10) DSV4_L1(11) DSV4_L1(12) DSV4_L1(13) DSV4_L1(14) DSV4_L1(15)
+        DSV4_L2(8) DSV4_L2(9) DSV4_L2(10) DSV4_L2(11) DSV4_L2(12) DSV4_L2(13) DSV4_L2(14) DSV4_L2(15) DSV4_L2(16)
+        default: return hipErrorInvalidValue;
+    }
+#undef DSV4_L1
+#undef DSV4_L2
+    return hipGetLastError();
+}
+
 hipError_t launch_multi_mfma(const MultiArgs& ma, int blocks, hipStream_t stream) {
     const dim3 grid((unsigned)blocks);
     switch (ma.base.K) {
@@ -915,24 +967,28 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
 
 int launch(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
+    const int long_blocks = long_mfma_blocks(a);
     if (tile_ok(a)) {
         const int rows = (int)std::min<int64_t>((int64_t)a.N * G, INT32_MAX);
         e = use_mfma(a.T, a.K, rows, a.xstride) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
                                      : launch_tile<1>(a, SwigluArgs{}, G, stream);
+    } else if (long_blocks > 0) {
+        e = launch_mfma_long(a, long_blocks, G, stream);
     } else {
         const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);
         const dim3 block(64 * kWaves);
         const int nc = (a.K + 1023) / 1024;
         const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) &&
                         (a.T == 1 || a.xstride % 8 == 0) && (a.xgroup % 8 == 0);
-#define DSV4_LAUNCH(NCV)                                                                    \
-    if (al) hipLaunchKernelGGL((fp8_gemv_kernel<NCV, true>), grid, block, 0, stream, a);   \
-    else hipLaunchKernelGGL((fp8_gemv_kernel<NCV, false>), grid, block, 0, stream, a);
+#define DSV4_LAUNCH(NCV, LV)                                                                    \
+    if (al) hipLaunchKernelGGL((fp8_gemv_kernel<NCV, true, LV>), grid, block, 0, stream, a);   \
+    else hipLaunchKernelGGL((fp8_gemv_kernel<NCV, false, LV>), grid, block, 0, stream, a);
         switch (nc) {
-            case 1: DSV4_LAUNCH(1) break;
-            case 2: DSV4_LAUNCH(2) break;
-            case 3: DSV4_LAUNCH(3) break;
-            default: DSV4_LAUNCH(4) break;
+            case 1: DSV4_LAUNCH(1, false) break;
+            case 2: DSV4_LAUNCH(2, false) break;
+            case 3: DSV4_LAUNCH(3, false) break;
+            case 4: DSV4_LAUNCH(4, false) break;
+            default: DSV4_LAUNCH(4, true) break;
         }
 #undef DSV4_LAUNCH
         e = hipGetLastError();

@@ -172,8 +172,10 @@ def test_fp8_gemv_tile_path_tokens_and_ragged_n(device, N, K, T):
                                               (45, 4096, 5, True), (20, 12288, 2, True)])
 def test_fp8_gemv_general_path(device, N, K, T, odd_stride):
     """K off the tile set (a multiple of 128 up to the 16384 cap; rows longer
-    than 4096 are walked in segments, once per token) and weight rows at an odd
-    byte stride (unaligned 16-byte loads): the general kernel, against the oracle."""
+    than 4096 are walked in segments, once per group of 8 tokens) and weight
+    rows at an odd byte stride (unaligned 16-byte loads): the general kernel,
+    against the oracle. Aligned rows longer than 4096 at T >= 2 take the
+    matrix cores (test_fp8_gemv_long_rows_matrix_cores)."""
     announce(f"fp8_e4m3_gemv general N={N} K={K} T={T} odd_stride={odd_stride}")
     w, s = synth.fp8_weight(4500 + N + K + T, N, K)
     x = synth.normal_bf16(4600 + T, (T, K))
@@ -186,6 +188,36 @@ def test_fp8_gemv_general_path(device, N, K, T, odd_stride):
     xd = dev_bf16(x, device)
     y = fp8b.fp8_e4m3_gemv(tw, dev_u8(s, device), xd if T > 1 else xd[0])
     assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 general N={N} K={K} T={T}")
+
+
+@pytest.mark.parametrize("N,K,T", [(576, 6144, 8), (1536, 12288, 8), (200, 16384, 16), (130, 4608, 3),
+                                   (64, 9216, 5), (300, 7680, 2)])
+def test_fp8_gemv_long_rows_matrix_cores(device, N, K, T):
+    """Aligned rows longer than the tile set (K a multiple of 512 above 4096,
+    other than 8192) with several tokens: the matrix-core kernel with one
+    wave per 512-k block (up to 15 blocks) or per two blocks (up to 32),
+    which reads each weight byte once for all tokens; against the oracle."""
+    announce(f"fp8_e4m3_gemv long rows on the matrix cores N={N} K={K} T={T}")
+    w, s = synth.fp8_weight(4700 + N + K + T, N, K)
+    x = synth.normal_bf16(4800 + T, (T, K))
+    y = fp8b.fp8_e4m3_gemv(dev_u8(w, device), dev_u8(s, device), dev_bf16(x, device))
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 long N={N} K={K} T={T}")
+
+
+@pytest.mark.parametrize("T", [8, 16])
+def test_fp8_gemv_long_rows_general_token_groups(device, T):
+    """Rows longer than 4096 at an odd byte stride (the general kernel's
+    segmented body): each segment is loaded once per group of 8 tokens; T = 16
+    takes two groups. Against the oracle, and equal to the aligned rows'
+    matrix-core result within the tolerance."""
+    N, K = 96, 12288
+    announce(f"fp8_e4m3_gemv general long rows N={N} K={K} T={T} odd stride")
+    w, s = synth.fp8_weight(4900 + T, N, K)
+    x = synth.normal_bf16(4950 + T, (T, K))
+    buf = torch.zeros(N, K + 1, dtype=torch.uint8, device=device)
+    buf[:, :K] = dev_u8(w, device)
+    y = fp8b.fp8_e4m3_gemv(buf[:, :K], dev_u8(s, device), dev_bf16(x, device))
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 general long T={T}")
 
 
 def test_fp8_gemv_long_rows_and_ragged_n(device):
