@@ -137,66 +137,73 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* w, co
     }
 }
 
-// Tile kernel for K in {2048, 4096, 8192} with 16-byte aligned rows and
-// activation. A workgroup of 256 threads owns R = C*256/KC rows (KC = K/32
-// blocks per row); thread t takes blocks t, t+256, ... of the workgroup's
-// [R, KC] block grid, so all of its blocks share one k-slice (block t % KC)
-// and every wave instruction reads 1 KiB of a single row. The activation
-// slice (32 bf16) is issued first, then the C weight blocks and scale bytes,
-// all unconditional (rows clamped), so one issue pass puts everything in
-// flight. Partials (C per wave, one butterfly) meet in LDS, fixed order.
-// The block scale is applied once per block: it is a power of two, so this
-// equals the per-element scaling of kernel/mxfp4-dense/mxfp4_gemv.cu:116-117
-// up to the rounding of partial sums.
-template <int C, int KC>
-__global__ __launch_bounds__(256) void mxfp4_gemv_tile_kernel(const GemvArgs a) {
-    constexpr int kRowsWG = C * 256 / KC;
-    __shared__ float part[kWaves][C];
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int n0 = blockIdx.x * kRowsWG;
-    const int b = t % KC;
-    uint32_t xs[16];
-    {
-        const u32x4* s4 = reinterpret_cast<const u32x4*>(a.x + b * kBlkElems);
+// Row kernel for K in {2048, 4096, 8192} with 16-byte aligned rows and
+// activation: each wave owns kFastRows consecutive rows, lane l takes MX
+// blocks l, l+64, ... (NB = K/2048 per row), so every wave load instruction
+// reads 1 KiB of one row and the activation slice (NB blocks of 32 bf16) is
+// loaded once per wave for both rows. Activation first, then the rows'
+// weight blocks and scale bytes, all unconditional (rows clamped), so one
+// issue pass puts everything in flight; each row is reduced by one butterfly
+// and stored by one lane: no LDS and no barrier. The block scale is applied
+// once per block: it is a power of two, so this equals the per-element
+// scaling of kernel/mxfp4-dense/mxfp4_gemv.cu:116-117 up to the rounding of
+// partial sums.
+// Workgroup L (dispatched to XCD L % 8) takes row block (L % 8) * (G / 8) +
+// L / 8 of the G = gridDim.x blocks (G a multiple of 8; blocks past the
+// matrix exit), so the workgroups that write one 128-byte line of y run on
+// one XCD. On MI355X (2048 x 4096, graph replay over 512 MB of weight
+// copies) this layout took 2.88 us against 3.05 for two-block tiles of 256
+// threads combined across waves in LDS (3.18-3.43 us with 4 or 8 rows per
+// wave, 2.94 us for the tiles with the XCD mapping alone).
+constexpr int kFastRows = 2;
+constexpr int kFastWaves = 4;
+
+template <int NB>
+__global__ __launch_bounds__(64 * kFastWaves) void mxfp4_gemv_rows_kernel(const GemvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int G = gridDim.x;
+    const int blk = (int)((blockIdx.x % 8) * (G / 8) + blockIdx.x / 8);
+    const int n0 = (blk * kFastWaves + wave) * kFastRows;
+    if (n0 >= a.N) return;
+    uint32_t xs[NB][16];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const u32x4* s4 = reinterpret_cast<const u32x4*>(a.x + (lane + 64 * j) * kBlkElems);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const u32x4 v = s4[q];
-            xs[4 * q] = v[0]; xs[4 * q + 1] = v[1]; xs[4 * q + 2] = v[2]; xs[4 * q + 3] = v[3];
+            xs[j][4 * q] = v[0]; xs[j][4 * q + 1] = v[1]; xs[j][4 * q + 2] = v[2]; xs[j][4 * q + 3] = v[3];
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // activation loads first
-    u32x4 w[C];
-    uint32_t sb[C];
+    u32x4 w[kFastRows][NB];
+    uint32_t sb[kFastRows][NB];
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-        const int n = min(n0 + (t + 256 * i) / KC, a.N - 1);
-        w[i] = ld16_stream(a.w + (int64_t)n * a.wrow + b * 16);
-        sb[i] = a.s[(int64_t)n * a.srow + b];
+    for (int r = 0; r < kFastRows; ++r) {
+        const int64_t n = min(n0 + r, a.N - 1);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            w[r][j] = ld16_stream(a.w + n * a.wrow + (int64_t)(lane + 64 * j) * 16);
+            sb[r][j] = a.s[n * a.srow + lane + 64 * j];
+        }
     }
-    float acc[C];
+    float acc[kFastRows];
     float chain = 0.f;
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-        reg_barrier_after(w[i], chain);
-        acc[i] = fp4_block_dot(w[i], xs) * e8m0_to_f32(sb[i]);
-        chain = acc[i];
-    }
-    wave_reduce_n<C>(acc, lane);
-    const int v = reduced_index<C>(lane);
-    if (reduced_owner<C>(lane)) part[wave][v] = acc[0];
-    __syncthreads();
-    if (t < kRowsWG && n0 + t < a.N) {
-        float sum = 0.f;
+    for (int r = 0; r < kFastRows; ++r) {
+        float s = 0.f;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
-#pragma unroll
-            for (int i = 0; i < C; ++i)
-                if ((64 * w2 + 256 * i) / KC == t) sum += part[w2][i];
+        for (int j = 0; j < NB; ++j) {
+            reg_barrier_after(w[r][j], chain);
+            s = fmaf(fp4_block_dot(w[r][j], xs[j]), e8m0_to_f32(sb[r][j]), s);
+            chain = s;
         }
-        a.y[n0 + t] = f32_to_bf16_bits(sum);
+        acc[r] = s;
     }
+    wave_reduce_n<kFastRows>(acc, lane);
+    const int v = reduced_index<kFastRows>(lane);
+    if (reduced_owner<kFastRows>(lane) && n0 + v < a.N) a.y[n0 + v] = f32_to_bf16_bits(acc[0]);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -222,13 +229,12 @@ extern "C" int mxfp4_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_packed, cons
                packed_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y)};
     const bool al = aligned16(x) && aligned16(W_packed) && (packed_row_stride_bytes % 16 == 0);
     if (al && (K == 2048 || K == 4096 || K == 8192)) {
-        // Two blocks per thread: 8, 4 or 2 rows per workgroup at K = 2048, 4096, 8192.
-        const int KC = K / kBlkElems;
-        const int rows = 2 * 256 / KC;
-        const dim3 g((unsigned)((N + rows - 1) / rows));
-        if (KC == 64) hipLaunchKernelGGL((mxfp4_gemv_tile_kernel<2, 64>), g, dim3(256), 0, stream, a);
-        else if (KC == 128) hipLaunchKernelGGL((mxfp4_gemv_tile_kernel<2, 128>), g, dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL((mxfp4_gemv_tile_kernel<2, 256>), g, dim3(256), 0, stream, a);
+        const int per_wg = kFastRows * kFastWaves;
+        const unsigned blocks = (unsigned)((N + per_wg - 1) / per_wg);
+        const dim3 g((blocks + 7u) / 8u * 8u);
+        if (K == 2048) hipLaunchKernelGGL(mxfp4_gemv_rows_kernel<1>, g, dim3(64 * kFastWaves), 0, stream, a);
+        else if (K == 4096) hipLaunchKernelGGL(mxfp4_gemv_rows_kernel<2>, g, dim3(64 * kFastWaves), 0, stream, a);
+        else hipLaunchKernelGGL(mxfp4_gemv_rows_kernel<4>, g, dim3(64 * kFastWaves), 0, stream, a);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
             std::fprintf(stderr, "mxfp4_gemv_m1 launch failed: %s\n", hipGetErrorString(e));
