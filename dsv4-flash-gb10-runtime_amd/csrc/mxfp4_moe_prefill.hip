@@ -260,29 +260,51 @@ __device__ __forceinline__ void dequant_block(u32x4 w, uint32_t s, bf16x8* op) {
     }
 }
 
-// The GEMM of one tile with NTB (1..4) blocks of 16 tokens. The weights of
-// the next DW super-steps and the activation pieces of the next DX are kept
-// in flight in registers: weights stream from HBM and need the deep ring;
-// activations are re-read by every row block of the tile and mostly hit L2.
-// Loads complete in issue order, so an activation piece issued DX steps
-// ahead is waited for together with every weight load issued before it:
-// one-block tiles, which have the registers, use DX = DW.
+// The GEMM of one tile with NTB (1..4) blocks of 16 tokens.
+// Weights: each wave owns 16 rows of the workgroup's 64 and reads them in
+// macro-steps of 256 k (128 bytes per row): two load instructions per
+// matrix, each giving lane l row 8q + l/8 of the wave's 16 and bytes
+// 16(l%8)..+15 of the macro-step, i.e. 8 whole 128-byte lines per
+// instruction. The wave writes those 16 rows x 128 B to its own LDS staging
+// area and reads back, as lane (r, g) (r = l%16, g = l/16), row r's blocks g
+// and g + 4: the MX blocks 4s + g of super-steps s = 2m and 2m + 1, the
+// operands of the MFMA layout. No other wave reads the area, so the
+// hand-over needs no barrier (LDS operations of one wave run in order; the
+// fences only keep the compiler from moving them). On MI355X, streaming the
+// stage-A weights of 251 experts this way ran at 7.1 TB/s, against 5.9 TB/s
+// when every load instruction takes the MFMA layout directly (16 rows x
+// 64 bytes: 16 half-used lines per instruction).
+// The weights of the next DW super-steps (DW/2 macro-steps) and the
+// activation pieces of the next DX super-steps are kept in flight in
+// registers: weights stream from HBM and need the deep ring; activations are
+// re-read by every row block of the tile and mostly hit L2. Loads complete in
+// issue order, so an activation piece issued DX steps ahead is waited for
+// together with every weight load issued before it: one-block tiles, which
+// have the registers, use DX = DW.
 // Each super-step's activation tile is written to one of two LDS buffers
 // before the barrier that precedes its multiply.
 // SFIX > 0: the super-step count is a compile-time constant and the loop is
 // unrolled completely; loads past the last super-step are then dropped at
 // compile time and every wait for an in-flight load is exact (a wait at the
 // top of a rolled loop covers all loads in flight). The rolled path (SFIX 0)
-// needs S to be a multiple of DW and clamps loads to the last super-step.
+// needs S to be a multiple of DW and clamps loads to the last macro-step.
 constexpr int kDepth = 4;   // super-steps per group of the rolled path (K granule = 512)
 constexpr int kDX = 2;
 constexpr int kDWDeep = 8;  // weight ring of the unrolled common-K bodies
+constexpr int kStgRow = 9;  // 16-byte slots per staged row (8 used: 144-byte stride)
+
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 template <bool TWO, int NTB, int SFIX, int DW, int DX>
 __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int p0, int n, int rb,
                                                   uint16_t (*xs)[kTileTok * kLdsRow],
-                                                  const int* s_row, uint8_t* sl) {
-    static_assert(DW % DX == 0 && (SFIX == 0 || SFIX % DW == 0), "ring depths");
+                                                  const int* s_row, uint8_t* sl, u32x4* stg) {
+    static_assert(DW % 2 == 0 && DW % DX == 0 && (SFIX == 0 || SFIX % DW == 0), "ring depths");
+    constexpr int DM = DW / 2;                        // weight ring in macro-steps
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -299,13 +321,21 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
     const __amdgpu_buffer_rsrc_t rbv = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(TWO ? a.wb + (int64_t)e * a.w_exp_stride + (int64_t)rb * blk_bytes : a.wa), (short)0, blk_bytes,
         0x00020000);
-    const int lrow = rl * (a.K / 2);
     const int S = SFIX > 0 ? SFIX : a.K / kStep;
+    const int SM = S / 2;                             // macro-steps
+    // this lane's line-layout piece: row 16*wave + 8q + lane/8, bytes 16*(lane%8) of each macro-step
+    const int lq = (wave * 16 + (lane >> 3)) * (a.K / 2) + (lane & 7) * 16;
+    const int lq8 = 8 * (a.K / 2);                    // + q * lq8 for the second instruction
 
     // Scale tile: the block's 64 scale rows of each matrix are one contiguous
-    // run of 64*nblk bytes; 16 bytes per thread per piece, staged in LDS
-    // (sl: matrix A, then matrix B) before the first barrier of the loop.
+    // run of 64*nblk bytes, read 16 bytes per thread per piece and staged in
+    // LDS (sl: matrix A, then matrix B) before the first barrier of the loop,
+    // each row padded by one dword (stride nblk + 4): the lanes of a scale
+    // read take rows r = 0..15 at one column, and the odd dword stride puts
+    // them in 16 different banks (at a stride of nblk bytes they all fell in
+    // one bank at K = 4096, a 16-way conflict).
     const int spieces = kTileRows * nblk / 16;          // per matrix: 256 .. 1024
+    const int srs = nblk + 4;                           // LDS row stride of the scale tile
     const u32x4* SAt = reinterpret_cast<const u32x4*>(a.sa + (int64_t)e * a.s_exp_stride + (int64_t)rb * kTileRows * nblk);
     const u32x4* SBt = TWO ? reinterpret_cast<const u32x4*>(a.sb + (int64_t)e * a.s_exp_stride + (int64_t)rb * kTileRows * nblk) : nullptr;
     // pieces per thread: exact for a compile-time K, else at the K cap
@@ -343,27 +373,40 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
 #pragma unroll
         for (int i = 0; i < NTB; ++i) xv[d][i] = *reinterpret_cast<const u32x4*>(xsrc[i] + so);
     };
-    u32x4 wa_r[DW], wb_r[DW];
-    auto load_w = [&](int d, int s) {
-        if (SFIX > 0 && s >= S) return;
-        const int blk = 4 * min(s, S - 1) + g;
-        wa_r[d] = __builtin_amdgcn_raw_buffer_load_b128(ra, lrow + blk * 16, 0, 0);
-        if constexpr (TWO) wb_r[d] = __builtin_amdgcn_raw_buffer_load_b128(rbv, lrow + blk * 16, 0, 0);
+    u32x4 la[DM][2], lb[DM][2];
+    auto load_w = [&](int d, int m) {
+        if (SFIX > 0 && m >= SM) return;
+        const int off = lq + min(m, SM - 1) * 128;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            la[d][q] = __builtin_amdgcn_raw_buffer_load_b128(ra, off + q * lq8, 0, 0);
+            if constexpr (TWO) lb[d][q] = __builtin_amdgcn_raw_buffer_load_b128(rbv, off + q * lq8, 0, 0);
+        }
     };
 #pragma unroll
     for (int d = 0; d < DX; ++d) load_x(d, d);
 #pragma unroll
-    for (int d = 0; d < DW; ++d) load_w(d, d);
+    for (int d = 0; d < DM; ++d) load_w(d, d);
     __builtin_amdgcn_sched_barrier(0);
-    u32x4* slv = reinterpret_cast<u32x4*>(sl);
+    const int ppr = nblk / 16;                          // 16-byte pieces per scale row
 #pragma unroll
     for (int i = 0; i < kSPer; ++i) {
         const int q = t + 256 * i;
-        if (q < (TWO ? 2 : 1) * spieces) slv[q] = sv[i];
+        if (q < (TWO ? 2 : 1) * spieces) {
+            const int row = q / ppr;                    // over matrix A's 64 rows, then B's
+            uint32_t* dst = reinterpret_cast<uint32_t*>(sl + row * srs + (q % ppr) * 16);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dst[c] = sv[i][c];
+        }
     }
     __syncthreads();  // the scale tile is read before each step's barrier
-    const uint8_t* sla = sl + rl * nblk + g;               // + 4*s: this lane's block of super-step s
-    const uint8_t* slb = sl + spieces * 16 + rl * nblk + g;
+    const uint8_t* sla = sl + rl * srs + g;                // + 4*s: this lane's block of super-step s
+    const uint8_t* slb = sl + kTileRows * srs + rl * srs + g;
+    // the wave's staging area: matrix A rows 0..15, then matrix B rows 0..15
+    u32x4* sta = stg + wave * (TWO ? 2 : 1) * 16 * kStgRow;
+    u32x4* stb = sta + 16 * kStgRow;
+    const int wslot = (lane >> 3) * kStgRow + (lane & 7);  // + 8 * kStgRow for q = 1
+    const int rslot = (lane & 15) * kStgRow + g;           // + 4 for the second super-step
 
     f32x4 acc_a[NTB], acc_b[NTB];
 #pragma unroll
@@ -372,37 +415,52 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
         acc_b[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int s0 = 0; s0 < (SFIX > 0 ? SFIX : S); s0 += DW) {
+    for (int m0 = 0; m0 < (SFIX > 0 ? SFIX / 2 : SM); m0 += DM) {
 #pragma unroll
-        for (int d = 0; d < DW; ++d) {
-            const int s = s0 + d;
-            const int dx = d % DX;
-            uint16_t* xb = xs[d & 1];          // s & 1 (s0 is a multiple of DW, DW even)
+        for (int dm = 0; dm < DM; ++dm) {
+            // macro-step m0 + dm: through the staging area into the MFMA layout
+            u32x4 wa_m[2], wb_m[2];
+            wave_lds_order();   // the previous macro-step's reads come first
 #pragma unroll
-            for (int i = 0; i < NTB; ++i) *reinterpret_cast<u32x4*>(xb + xoff[i]) = xv[dx][i];
-            load_x(dx, s + DX);
-            const u32x4 wa_c = wa_r[d];
-            u32x4 wb_c{};
-            if constexpr (TWO) wb_c = wb_r[d];
-            load_w(d, s + DW);
-            // The dequantisation needs only this wave's registers and the
-            // scale tile, so it runs before the barrier and overlaps the wait
-            // for the other waves' activation pieces.
-            const uint32_t sa_c = sla[4 * s];
-            const uint32_t sb_c = TWO ? slb[4 * s] : 0u;
-            bf16x8 opa[4], opb[4];
-            dequant_block(wa_c, sa_c, opa);
-            if constexpr (TWO) dequant_block(wb_c, sb_c, opb);
-            __syncthreads();
+            for (int q = 0; q < 2; ++q) {
+                sta[wslot + q * 8 * kStgRow] = la[dm][q];
+                if constexpr (TWO) stb[wslot + q * 8 * kStgRow] = lb[dm][q];
+            }
+            wave_lds_order();
 #pragma unroll
-            for (int b = 0; b < NTB; ++b) {
-                const uint16_t* xrow = xb + (16 * b + (lane & 15)) * kLdsRow + 32 * g;
+            for (int h = 0; h < 2; ++h) {
+                wa_m[h] = sta[rslot + 4 * h];
+                if constexpr (TWO) wb_m[h] = stb[rslot + 4 * h];
+            }
+            load_w(dm, m0 + dm + DM);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bf16x8 xop = *reinterpret_cast<const bf16x8*>(xrow + 8 * j);
-                    acc_a[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(opa[j], xop, acc_a[b], 0, 0, 0);
-                    if constexpr (TWO)
-                        acc_b[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(opb[j], xop, acc_b[b], 0, 0, 0);
+            for (int h = 0; h < 2; ++h) {
+                const int d = 2 * dm + h;            // super-step within the DW group
+                const int s = 2 * m0 + d;
+                const int dx = d % DX;
+                uint16_t* xb = xs[d & 1];            // s & 1 (m0 a multiple of DM, so 2*m0 is even)
+#pragma unroll
+                for (int i = 0; i < NTB; ++i) *reinterpret_cast<u32x4*>(xb + xoff[i]) = xv[dx][i];
+                load_x(dx, s + DX);
+                // The dequantisation needs only this wave's registers and the
+                // scale tile, so it runs before the barrier and overlaps the
+                // wait for the other waves' activation pieces.
+                const uint32_t sa_c = sla[4 * s];
+                const uint32_t sb_c = TWO ? slb[4 * s] : 0u;
+                bf16x8 opa[4], opb[4];
+                dequant_block(wa_m[h], sa_c, opa);
+                if constexpr (TWO) dequant_block(wb_m[h], sb_c, opb);
+                __syncthreads();
+#pragma unroll
+                for (int b = 0; b < NTB; ++b) {
+                    const uint16_t* xrow = xb + (16 * b + (lane & 15)) * kLdsRow + 32 * g;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const bf16x8 xop = *reinterpret_cast<const bf16x8*>(xrow + 8 * j);
+                        acc_a[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(opa[j], xop, acc_a[b], 0, 0, 0);
+                        if constexpr (TWO)
+                            acc_b[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(opb[j], xop, acc_b[b], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -436,12 +494,17 @@ __device__ __forceinline__ void prefill_gemm_tile(const GemmArgs& a, int e, int 
 // workgroup, k = L / 8, takes row block k % RB of tile 8 * (k / RB) + L % 8,
 // so one tile's row blocks run back to back on one XCD and share its L2
 // copy of the tile's activation rows. TWO: stage A (W1 and W3, SwiGLU
-// epilogue into M); otherwise stage B (W2, weighted fp32 rows into Y). The
-// tile's token-block count selects a specialised body.
-template <bool TWO>
+// epilogue into M); otherwise stage B (W2, weighted fp32 rows into Y). SFIX:
+// the super-step count K / 128 when it is 4, 16 or 32 (unrolled bodies, the
+// scale tile sized for that K), else 0 (rolled body, scale tile at the K
+// cap). The tile's token-block count selects a specialised body.
+template <bool TWO, int SFIX>
 __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a, int RB) {
+    constexpr int kNblkMax = SFIX > 0 ? 4 * SFIX : kMaxRed / kBlk;
+    constexpr int kMats = TWO ? 2 : 1;
     __shared__ __align__(16) uint16_t xs[2][kTileTok * kLdsRow];   // 2 x 17 KB
-    __shared__ __align__(16) uint8_t sl[(TWO ? 2 : 1) * kTileRows * (kMaxRed / kBlk)];
+    __shared__ __align__(16) uint8_t sl[kMats * kTileRows * (kNblkMax + 4)];
+    __shared__ u32x4 stg[4 * kMats * 16 * kStgRow];                 // 4.5 KB per wave and matrix
     __shared__ int s_row[kTileTok];
     const int L = blockIdx.x;
     const int k = L >> 3;
@@ -457,21 +520,15 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(const GemmArgs a, 
         s_row[t] = a.act_by_token ? a.pair_tok[p] : p;
     }
     __syncthreads();
-    const int S = a.K / kStep;
-// One-block tiles (most tiles of a prefill chunk) keep as many activation
-// pieces in flight as weight super-steps.
-#define DSV4_TILES(SV, DW)                                                                        \
-    switch ((n + 15) / 16) {                                                                      \
-        case 1: prefill_gemm_tile<TWO, 1, SV, DW, DW>(a, e, p0, n, rb, xs, s_row, sl); break;   \
-        case 2: prefill_gemm_tile<TWO, 2, SV, DW, kDX>(a, e, p0, n, rb, xs, s_row, sl); break;  \
-        case 3: prefill_gemm_tile<TWO, 3, SV, DW, kDX>(a, e, p0, n, rb, xs, s_row, sl); break;  \
-        default: prefill_gemm_tile<TWO, 4, SV, DW, kDX>(a, e, p0, n, rb, xs, s_row, sl); break; \
+    // One-block tiles (most tiles of a prefill chunk) keep as many activation
+    // pieces in flight as weight super-steps.
+    constexpr int DW = (SFIX == 16 || SFIX == 32) ? kDWDeep : kDepth;
+    switch ((n + 15) / 16) {
+        case 1: prefill_gemm_tile<TWO, 1, SFIX, DW, DW>(a, e, p0, n, rb, xs, s_row, sl, stg); break;
+        case 2: prefill_gemm_tile<TWO, 2, SFIX, DW, kDX>(a, e, p0, n, rb, xs, s_row, sl, stg); break;
+        case 3: prefill_gemm_tile<TWO, 3, SFIX, DW, kDX>(a, e, p0, n, rb, xs, s_row, sl, stg); break;
+        default: prefill_gemm_tile<TWO, 4, SFIX, DW, kDX>(a, e, p0, n, rb, xs, s_row, sl, stg); break;
     }
-    if (S == 32) { DSV4_TILES(32, kDWDeep) }
-    else if (S == 16) { DSV4_TILES(16, kDWDeep) }
-    else if (S == 4) { DSV4_TILES(4, kDepth) }
-    else { DSV4_TILES(0, kDepth) }
-#undef DSV4_TILES
 }
 
 // out[t, o] = bf16( sum_k Y[pos(t, k), o] ), k in order; grid = (T, O / 1024).
@@ -496,6 +553,17 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* Y, co
 // ---------------------------------------------------------------- host ----
 
 uintptr_t align_up(uintptr_t v, uintptr_t a) { return (v + a - 1) / a * a; }
+
+// The stage kernel for the reduction length a.K (super-steps of 128).
+template <bool TWO>
+void launch_gemm(const GemmArgs& a, dim3 grid, int RB, hipStream_t stream) {
+    switch (a.K / kStep) {
+        case 32: hipLaunchKernelGGL((prefill_gemm_kernel<TWO, 32>), grid, dim3(256), 0, stream, a, RB); break;
+        case 16: hipLaunchKernelGGL((prefill_gemm_kernel<TWO, 16>), grid, dim3(256), 0, stream, a, RB); break;
+        case 4: hipLaunchKernelGGL((prefill_gemm_kernel<TWO, 4>), grid, dim3(256), 0, stream, a, RB); break;
+        default: hipLaunchKernelGGL((prefill_gemm_kernel<TWO, 0>), grid, dim3(256), 0, stream, a, RB); break;
+    }
+}
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct PrefillLayout {
@@ -641,8 +709,7 @@ extern "C" int mxfp4_moe_prefill(const dsv4_bf16_t* x, const uint8_t* W1_packed,
     A.pair_w = pt.pair_w;
     A.M = M;
     const unsigned tiles8 = (unsigned)((L.max_tiles + 7) / 8 * 8);
-    hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(tiles8 * (unsigned)(hidden / kTileRows)), dim3(256), 0,
-                       stream, A, hidden / kTileRows);
+    launch_gemm<true>(A, dim3(tiles8 * (unsigned)(hidden / kTileRows)), hidden / kTileRows, stream);
     if (hipGetLastError() != hipSuccess) return -6;
 
     GemmArgs B = A;
@@ -659,8 +726,7 @@ extern "C" int mxfp4_moe_prefill(const dsv4_bf16_t* x, const uint8_t* W1_packed,
     B.rows = out_dim;
     B.M = nullptr;
     B.Y = Y;
-    hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(tiles8 * (unsigned)(out_dim / kTileRows)), dim3(256), 0,
-                       stream, B, out_dim / kTileRows);
+    launch_gemm<false>(B, dim3(tiles8 * (unsigned)(out_dim / kTileRows)), out_dim / kTileRows, stream);
     if (hipGetLastError() != hipSuccess) return -7;
 
     hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)T, (unsigned)((out_dim / 4 + 255) / 256)),
