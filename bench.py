@@ -463,6 +463,21 @@ def dense_kernels(torch, dev, cpu: bool, counters: bool = False) -> dict:
             out[f"fp8_e4m3_gemv {N}x{Kf} T={T}"] = entry(us, wbytes + T * (2 * Kf + 2 * N),
                                                           cpu_us(lambda: mx.fp8_gemv(xh, w, ws)))
         del W, WS
+    # configs[2] with its literal scale format: one fp32 scale per 128x128
+    # block (fp8_e4m3_gemv_f32s; the reference ABI above carries E8M0 bytes)
+    for (N, Kf) in ((1536, 4096), (576, 4096), (4096, 4096), (4096, 2048)):
+        w, wsf = synth.fp8_weight_f32s(1702 + N + Kf, N, Kf)
+        wbytes = N * Kf + 4 * wsf.size
+        W, nW = copies(u8(w), wbytes)
+        WS = rep(torch.from_numpy(wsf).to(dev), nW)
+        for T in (1, 8):
+            xh = synth.normal_bf16(2002 + T, (T, Kf))
+            xdt = bf(xh) if T > 1 else bf(xh[0])
+            y = torch.empty((T, N) if T > 1 else (N,), dtype=torch.bfloat16, device=dev)
+            us = time_launches(lambda i: fp8b.fp8_e4m3_gemv_f32s(W[i], WS[i], xdt, out=y), nW)
+            out[f"fp8_e4m3_gemv_f32s {N}x{Kf} T={T}"] = entry(us, wbytes + T * (2 * Kf + 2 * N),
+                                                               cpu_us(lambda: mx.fp8_gemv_f32s(xh, w, wsf)))
+        del W, WS
     # Rows longer than the tile set (K up to the reference's 16384 cap) with
     # several tokens: each weight byte is read once for all tokens.
     for (N, Kf) in ((2048, 6144), (1024, 12288)):
@@ -620,6 +635,9 @@ def traffic_key(name: str):
     m = re.match(r"fp8_e4m3_gemv (?:wq_b |wo_b )?(\d+)x(\d+) T=(\d+)$", name)
     if m:
         return f"fp8_gemv_{m.group(1)}x{m.group(2)}@T{m.group(3)}"
+    m = re.match(r"fp8_e4m3_gemv_f32s (\d+)x(\d+) T=(\d+)$", name)
+    if m:
+        return f"fp8_gemv_f32s_{m.group(1)}x{m.group(2)}@T{m.group(3)}"
     m = re.match(r"rmsnorm_fuse_residual_add T=(\d+)x\d+$", name)
     if m:
         return f"rmsnorm_fuse_residual_add@T{m.group(1)}"
@@ -1018,8 +1036,11 @@ def summary(r: dict) -> dict:
              "router_logits bf16 256x4096 T=1": "router_gemv"}
     for name, e in (r.get("kernels") or {}).items():
         m = re.match(r"fp8_e4m3_gemv (?:(wq_b|wo_b) )?(\d+)x(\d+) T=(\d+)$", name)
+        mf = re.match(r"fp8_e4m3_gemv_f32s (\d+)x(\d+) T=(\d+)$", name)
         if m:
             key = f"fp8_{m.group(2)}x{m.group(3)}_T{m.group(4)}"
+        elif mf:
+            key = f"fp8f32s_{mf.group(1)}x{mf.group(2)}_T{mf.group(3)}"
         else:
             m = re.match(r"rmsnorm_fuse_residual_add T=(\d+)x\d+$", name)
             key = f"cfg1_rmsnorm_T{m.group(1)}" if m else short.get(name)

@@ -69,6 +69,22 @@ __device__ __forceinline__ u32x4 load_w16(const uint8_t* p) {
     else return ld16_unaligned(p);
 }
 
+// Tile-scale formats: SF = 0, E8M0 bytes (the reference ABI,
+// fp8_e4m3_gemv.cu:55-62); SF = 1, fp32 values (fp8_e4m3_gemv_f32s). A scale
+// is loaded as its raw 32-bit pattern (the byte, or the float's bits) and
+// turned into an fp32 multiplier where it is applied.
+template <int SF>
+__device__ __forceinline__ uint32_t scale_raw(const uint8_t* s, int64_t idx) {
+    if constexpr (SF == 1) return reinterpret_cast<const uint32_t*>(s)[idx];
+    else return s[idx];
+}
+
+template <int SF>
+__device__ __forceinline__ float scale_value(uint32_t raw) {
+    if constexpr (SF == 1) return __uint_as_float(raw);
+    else return e8m0_to_f32(raw);
+}
+
 // grid = ceil(N / (kWaves*kRows)), block = 64*kWaves. A row is walked in
 // segments of NC*1024 bytes (NC 16-byte chunks per lane, NC <= 4). With one
 // segment (K <= 4096) the rows stay in registers across all T tokens;
@@ -80,7 +96,7 @@ __device__ __forceinline__ u32x4 load_w16(const uint8_t* p) {
 // one-segment kernels keep their smaller register budget.
 constexpr int kGenTok = 8;
 
-template <int NC, bool ALIGNED, bool LONG>
+template <int NC, bool ALIGNED, bool LONG, int SF = 0>
 __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -101,7 +117,7 @@ __global__ __launch_bounds__(64 * kWaves) void fp8_gemv_kernel(const Fp8Args a) 
                 if (n < a.N && k < a.K) {
                     const int64_t gn = gv.row0 + n;
                     wv[r][j] = load_w16<ALIGNED>(a.w + gn * a.wrow + k);
-                    sc[r][j] = e8m0_to_f32(a.s[(gn / kTile) * a.srow + k / kTile]);
+                    sc[r][j] = scale_value<SF>(scale_raw<SF>(a.s, (gn / kTile) * a.srow + k / kTile));
                 } else {
                     wv[r][j] = u32x4{0u, 0u, 0u, 0u};
                     sc[r][j] = 0.f;
@@ -210,9 +226,10 @@ struct TileShape {
 
 // The body shared by the single-matrix, grouped and multi-matrix launches:
 // workgroup `blk` of the matrix described by `a` and `gv`.
-template <int C, int TT, int KC, int MAT>
+template <int C, int TT, int KC, int MAT, int SF = 0>
 __device__ __forceinline__ void fp8_tile_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
                                               int blk, float (*part)[MAT][C][TT]) {
+    static_assert(SF == 0 || MAT == 1, "fp32 tile scales on the single-matrix kernel only");
     using S = TileShape<C, TT, KC, MAT>;
     constexpr int kRowsWG = S::kRowsWG, KS = S::KS, kVals = S::kVals;
     const int t = threadIdx.x;
@@ -244,7 +261,7 @@ __device__ __forceinline__ void fp8_tile_body(const Fp8Args& a, const SwigluArgs
         const int64_t gn = gv.row0 + min(n0 + (t + 256 * i) / KC, a.N - 1);
         const int k = kb + 4096 * (i % KS);
         w[0][i] = ld16_stream(a.w + gn * a.wrow + k);
-        sb[0][i] = a.s[(gn / kTile) * a.srow + k / kTile];
+        sb[0][i] = scale_raw<SF>(a.s, (gn / kTile) * a.srow + k / kTile);
         if constexpr (MAT == 2) {
             w[1][i] = ld16_stream(sw.w3 + gn * a.wrow + k);
             sb[1][i] = sw.s3[(gn / kTile) * a.srow + k / kTile];
@@ -260,7 +277,7 @@ __device__ __forceinline__ void fp8_tile_body(const Fp8Args& a, const SwigluArgs
             float acc[kVals];
 #pragma unroll
             for (int i = 0; i < C; ++i) {
-                const float sc = e8m0_to_f32(sb[m][i]);
+                const float sc = m == 0 ? scale_value<SF>(sb[m][i]) : e8m0_to_f32(sb[m][i]);
 #pragma unroll
                 for (int tok = 0; tok < TT; ++tok) acc[i * TT + tok] = fp8_chunk_dot(w[m][i], xp[tok][i % KS]) * sc;
             }
@@ -299,10 +316,10 @@ __device__ __forceinline__ void fp8_tile_body(const Fp8Args& a, const SwigluArgs
 }
 
 // One matrix, or G row groups of one matrix (blockIdx.y, GroupView).
-template <int C, int TT, int KC, int MAT>
+template <int C, int TT, int KC, int MAT, int SF = 0>
 __global__ __launch_bounds__(256) void fp8_gemv_tile_kernel(const Fp8Args a, const SwigluArgs sw) {
     __shared__ float part[kWaves][MAT][C][TT];
-    fp8_tile_body<C, TT, KC, MAT>(a, sw, group_view(a), blockIdx.x, part);
+    fp8_tile_body<C, TT, KC, MAT, SF>(a, sw, group_view(a), blockIdx.x, part);
 }
 
 // Several matrices that read the same activation (the pointer table of
@@ -786,15 +803,15 @@ int tile_tt(int T, int K, int MAT) {
 
 // Launch the tile kernel for TT tokens per group at the row length K (K = 8192
 // only with TT <= 4: tile_tt never asks for more there).
-template <int TT, int MAT>
+template <int TT, int MAT, int SF = 0>
 void launch_tile_tt(const Fp8Args& a, const SwigluArgs& sw, dim3 grid, hipStream_t stream) {
     switch (a.K) {
-        case 1024: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(1024), TT, 64, MAT>), grid, dim3(256), 0, stream, a, sw); break;
-        case 2048: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(2048), TT, 128, MAT>), grid, dim3(256), 0, stream, a, sw); break;
-        case 4096: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(4096), TT, 256, MAT>), grid, dim3(256), 0, stream, a, sw); break;
+        case 1024: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(1024), TT, 64, MAT, SF>), grid, dim3(256), 0, stream, a, sw); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(2048), TT, 128, MAT, SF>), grid, dim3(256), 0, stream, a, sw); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(4096), TT, 256, MAT, SF>), grid, dim3(256), 0, stream, a, sw); break;
         default:
             if constexpr (TT <= 4)
-                hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(8192), TT, 512, MAT>), grid, dim3(256), 0, stream, a, sw);
+                hipLaunchKernelGGL((fp8_gemv_tile_kernel<tile_c(8192), TT, 512, MAT, SF>), grid, dim3(256), 0, stream, a, sw);
             break;
     }
 }
@@ -813,16 +830,16 @@ void launch_multi_tt(const MultiArgs& ma, dim3 grid, hipStream_t stream) {
 }
 
 // G groups (grid.y). MAT = 2: the fused SwiGLU.
-template <int MAT>
+template <int MAT, int SF = 0>
 hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
     const dim3 grid((unsigned)((a.N + tile_rows(a.K) - 1) / tile_rows(a.K)), (unsigned)G);
     switch (tile_tt(a.T, a.K, MAT)) {
-        case 1: launch_tile_tt<1, MAT>(a, sw, grid, stream); break;
-        case 2: launch_tile_tt<2, MAT>(a, sw, grid, stream); break;
-        case 4: launch_tile_tt<4, MAT>(a, sw, grid, stream); break;
-        case 8: launch_tile_tt<8, MAT>(a, sw, grid, stream); break;
+        case 1: launch_tile_tt<1, MAT, SF>(a, sw, grid, stream); break;
+        case 2: launch_tile_tt<2, MAT, SF>(a, sw, grid, stream); break;
+        case 4: launch_tile_tt<4, MAT, SF>(a, sw, grid, stream); break;
+        case 8: launch_tile_tt<8, MAT, SF>(a, sw, grid, stream); break;
         default:
-            if constexpr (MAT == 1) launch_tile_tt<16, MAT>(a, sw, grid, stream);
+            if constexpr (MAT == 1) launch_tile_tt<16, MAT, SF>(a, sw, grid, stream);
             break;
     }
     return hipGetLastError();
@@ -965,13 +982,16 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
     return hipGetLastError();
 }
 
-int launch(const Fp8Args& a, int G, hipStream_t stream) {
+// SF = 1 (fp32 tile scales) takes the vector kernels only: the tile kernel
+// for the tile shapes, the general kernel otherwise.
+template <int SF>
+int launch_sf(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
-    const int long_blocks = long_mfma_blocks(a);
+    const int long_blocks = SF == 0 ? long_mfma_blocks(a) : 0;
     if (tile_ok(a)) {
         const int rows = (int)std::min<int64_t>((int64_t)a.N * G, INT32_MAX);
-        e = use_mfma(a.T, a.K, rows, a.xstride) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
-                                     : launch_tile<1>(a, SwigluArgs{}, G, stream);
+        e = (SF == 0 && use_mfma(a.T, a.K, rows, a.xstride)) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
+                                                            : launch_tile<1, SF>(a, SwigluArgs{}, G, stream);
     } else if (long_blocks > 0) {
         e = launch_mfma_long(a, long_blocks, G, stream);
     } else {
@@ -980,9 +1000,9 @@ int launch(const Fp8Args& a, int G, hipStream_t stream) {
         const int nc = (a.K + 1023) / 1024;
         const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) &&
                         (a.T == 1 || a.xstride % 8 == 0) && (a.xgroup % 8 == 0);
-#define DSV4_LAUNCH(NCV, LV)                                                                    \
-    if (al) hipLaunchKernelGGL((fp8_gemv_kernel<NCV, true, LV>), grid, block, 0, stream, a);   \
-    else hipLaunchKernelGGL((fp8_gemv_kernel<NCV, false, LV>), grid, block, 0, stream, a);
+#define DSV4_LAUNCH(NCV, LV)                                                                        \
+    if (al) hipLaunchKernelGGL((fp8_gemv_kernel<NCV, true, LV, SF>), grid, block, 0, stream, a);   \
+    else hipLaunchKernelGGL((fp8_gemv_kernel<NCV, false, LV, SF>), grid, block, 0, stream, a);
         switch (nc) {
             case 1: DSV4_LAUNCH(1, false) break;
             case 2: DSV4_LAUNCH(2, false) break;
@@ -999,6 +1019,8 @@ int launch(const Fp8Args& a, int G, hipStream_t stream) {
     }
     return 0;
 }
+
+int launch(const Fp8Args& a, int G, hipStream_t stream) { return launch_sf<0>(a, G, stream); }
 
 }  // namespace
 
@@ -1027,6 +1049,26 @@ extern "C" int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const u
               weight_row_stride_bytes, scale_row_stride_bytes, reinterpret_cast<uint16_t*>(y),
               y_row_stride, 0, 0};
     return launch(a, 1, stream);
+}
+
+extern "C" int fp8_e4m3_gemv_f32s(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
+                                  const float* W_scale, int K, int N, int T, int64_t weight_row_stride_bytes,
+                                  int64_t scale_row_stride, dsv4_bf16_t* y, int64_t y_row_stride,
+                                  hipStream_t stream) {
+    const int v = validate(K, N);
+    if (v != 0) return v;
+    if (T < 1 || T > kMaxT) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_f32s: T=%d outside [1, %d]\n", T, kMaxT);
+        return -5;
+    }
+    if (!operands_set("fp8_e4m3_gemv_f32s", {x, W_fp8, W_scale, y})) return kNullOperand;
+    if ((reinterpret_cast<uintptr_t>(W_scale) & 3u) != 0 || scale_row_stride < K / kTile) {
+        std::fprintf(stderr, "fp8_e4m3_gemv_f32s: scales must be 4-byte aligned fp32 with a row stride >= K/128\n");
+        return -6;
+    }
+    Fp8Args a{reinterpret_cast<const uint16_t*>(x), x_row_stride, W_fp8, reinterpret_cast<const uint8_t*>(W_scale),
+              K, N, T, weight_row_stride_bytes, scale_row_stride, reinterpret_cast<uint16_t*>(y), y_row_stride, 0, 0};
+    return launch_sf<1>(a, 1, stream);
 }
 
 extern "C" int fp8_e4m3_gemv_grouped(const dsv4_bf16_t* x, int64_t x_row_stride, int64_t x_group_stride,

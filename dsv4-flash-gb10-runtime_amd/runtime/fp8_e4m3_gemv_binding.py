@@ -56,6 +56,8 @@ def _load_lib() -> ctypes.CDLL:
         lib.fp8_e4m3_rmsnorm_gemv.restype = I
         lib.fp8_e4m3_gemv_multi.argtypes = [P, L, I, I, I] + [P] * 7 + [P]
         lib.fp8_e4m3_gemv_multi.restype = I
+        lib.fp8_e4m3_gemv_f32s.argtypes = [P, L, P, P, I, I, I, L, L, P, L, P]
+        lib.fp8_e4m3_gemv_f32s.restype = I
         _LIB = lib
     return _LIB
 
@@ -122,6 +124,49 @@ def fp8_e4m3_gemv(
         name = "fp8_e4m3_gemv"
     if rc != 0:
         raise RuntimeError(f"{name} returned {rc}")
+    return out
+
+
+def fp8_e4m3_gemv_f32s(
+    W_fp8: torch.Tensor,
+    W_scale: torch.Tensor,
+    x: torch.Tensor,
+    out: Optional[torch.Tensor] = None,
+    stream: Optional[torch.cuda.Stream] = None,
+) -> torch.Tensor:
+    """fp8_e4m3_gemv with one fp32 scale per 128x128 tile (W_scale float32
+    [ceil(N/128), K/128], rows contiguous) instead of E8M0 bytes: y = x @
+    (e4m3(W) * S).T for x [K] (y [N]) or x [T, K] (y [T, N]); fp32 accumulate."""
+    if not (W_fp8.is_cuda and W_scale.is_cuda and x.is_cuda):
+        raise RuntimeError("all tensors must be on a GPU device")
+    if W_fp8.dtype != torch.uint8:
+        raise RuntimeError(f"W_fp8 must be uint8 (E4M3FN bits), got {W_fp8.dtype}")
+    if W_scale.dtype != torch.float32:
+        raise RuntimeError(f"W_scale must be float32, got {W_scale.dtype}")
+    if W_fp8.dim() != 2 or W_scale.dim() != 2 or W_fp8.stride(1) != 1 or W_scale.stride(1) != 1:
+        raise RuntimeError("W_fp8 and W_scale must be 2-D with contiguous rows")
+    N, K = W_fp8.shape
+    if tuple(W_scale.shape) != ((N + 127) // 128, K // 128):
+        raise RuntimeError(f"W_scale must be [{(N + 127) // 128}, {K // 128}], got {tuple(W_scale.shape)}")
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError(f"x must be bfloat16, got {x.dtype}")
+    if x.dim() not in (1, 2) or x.shape[-1] != K:
+        raise RuntimeError(f"x must be [K] or [T, K] with K={K}, got shape {tuple(x.shape)}")
+    T = 1 if x.dim() == 1 else x.shape[0]
+    if T > MAX_TOKENS:
+        raise RuntimeError(f"T={T} > {MAX_TOKENS}")
+    x = x.contiguous()
+    oshape = (N,) if x.dim() == 1 else (T, N)
+    if out is None:
+        out = torch.empty(oshape, dtype=torch.bfloat16, device=x.device)
+    elif tuple(out.shape) != oshape or out.dtype != torch.bfloat16 or not out.is_cuda \
+            or not out.is_contiguous():
+        raise RuntimeError(f"out must be a contiguous GPU bfloat16 {oshape} tensor")
+    s = ctypes.c_void_p(_lib.stream_ptr(x.device, stream))
+    rc = _load_lib().fp8_e4m3_gemv_f32s(_lib.vp(x), K, _lib.vp(W_fp8), _lib.vp(W_scale), K, N, T,
+                                        W_fp8.stride(0), W_scale.stride(0), _lib.vp(out), N, s)
+    if rc != 0:
+        raise RuntimeError(f"fp8_e4m3_gemv_f32s returned {rc}")
     return out
 
 

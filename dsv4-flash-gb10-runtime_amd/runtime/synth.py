@@ -140,6 +140,23 @@ def fp8_weight(seed: int, N: int, K: int, std: float = 0.02):
     return codes, scale_b
 
 
+def fp8_weight_f32s(seed: int, N: int, K: int, std: float = 0.02):
+    """E4M3FN codes [N, K] and fp32 tile scales [ceil(N/128), K/128] of N(0, std)
+    weights, one scale per 128x128 block: amax / 448 (the benchmark's FP8
+    configuration), codes = RNE-to-E4M3(W / scale)."""
+    w = std * normal_f64(seed, 0, N * K).reshape(N, K)
+    nt, kt = (N + 127) // 128, K // 128
+    pad = np.zeros((nt * 128, K))
+    pad[:N] = w
+    amax = np.abs(pad.reshape(nt, 128, kt, 128)).max(axis=(1, 3))
+    scale = np.where(amax > 0, amax / 448.0, 1.0).astype(np.float32)
+    sfull = np.repeat(np.repeat(scale.astype(np.float64), 128, axis=0), 128, axis=1)[:N, :K]
+    # the scale rounded to fp32 can put the block's largest value a rounding
+    # step above 448: saturate at the largest E4M3FN value
+    codes = e4m3fn_quantize(np.clip(w / sfull, -448.0, 448.0))
+    return codes, scale
+
+
 # ---------------------------------------------------------------- routing ---
 
 def gating_logits(seed: int, T: int, n_experts: int) -> np.ndarray:

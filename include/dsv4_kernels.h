@@ -13,7 +13,8 @@
  *   kernel/fp8-dense/libfp8_e4m3_gemv.so          fp8_e4m3_gemv_m1,
  *                                                 fp8_e4m3_gemv, fp8_e4m3_gemv_grouped,
  *                                                 fp8_e4m3_gemv_multi,
- *                                                 fp8_e4m3_swiglu_gemv, fp8_e4m3_rmsnorm_gemv,
+ *                                                 fp8_e4m3_gemv_f32s, fp8_e4m3_swiglu_gemv,
+ *                                                 fp8_e4m3_rmsnorm_gemv,
  *                                                 fp8_e4m3_dequant_bf16 (extensions)
  *   kernel/rmsnorm-fuse/librmsnorm_fuse.so        rmsnorm_fuse_fwd,
  *                                                 rmsnorm_fuse_residual_add
@@ -311,6 +312,22 @@ int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_f
                   const uint8_t* W_scale, int K, int N, int T,
                   int64_t weight_row_stride_bytes, int64_t scale_row_stride_bytes,
                   dsv4_bf16_t* y, int64_t y_row_stride, hipStream_t stream);
+
+/* EXTENSION: fp8_e4m3_gemv with one fp32 scale per 128x128 tile, W_scale
+ * float [ceil(N/128), K/128] with row stride scale_row_stride (in floats, at
+ * least K/128), 4-byte aligned: the scale format of the benchmark's FP8
+ * configuration, where the reference ABI (kernel/fp8-dense/fp8_e4m3_gemv.cu:
+ * 132-142, runtime/fp8_e4m3_gemv_binding.py:88) carries E8M0 bytes and the
+ * reference's dequantisation (runtime/dsv4_engine_mxfp4.py:531-553) multiplies
+ * e4m3(W) by the tile's scale in fp32 before rounding to bf16. The scale
+ * multiplies each 16-element partial dot (fp32), so results agree with that
+ * dequantise-then-multiply path within fp32/bf16 rounding. Vector kernels
+ * only (no matrix-core path). Return codes as fp8_e4m3_gemv, plus -6 for a
+ * misaligned scale pointer or a scale row stride below K/128. */
+int fp8_e4m3_gemv_f32s(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
+                       const float* W_scale, int K, int N, int T, int64_t weight_row_stride_bytes,
+                       int64_t scale_row_stride, dsv4_bf16_t* y, int64_t y_row_stride,
+                       hipStream_t stream);
 
 /* EXTENSION (replaces the per-group loop of 8 fp8_e4m3_gemv_m1 calls for the
  * grouped output projection wo_a, reference

@@ -154,6 +154,22 @@ def fp8_dequant_bf16(w, s, kernel_convention: bool = True) -> np.ndarray:
         return bf16_round(e4m3fn_decode(w) * full)
 
 
+def fp8_dequant_bf16_f32s(w, s_f32) -> np.ndarray:
+    """[N, K] E4M3FN + [ceil(N/128), K/128] fp32 tile scales -> [N, K] bf16
+    bits: bf16(fp32(e4m3(w) * S[n/128, k/128])), the product rounded to fp32
+    and then to bf16, as runtime/dsv4_engine_mxfp4.py:539-548 does with a
+    float scale (the benchmark's FP8 configuration).
+
+    Pinned: tests compare with torch's float8_e4m3fn view times a float32
+    scale, cast to bfloat16."""
+    w = np.asarray(w, dtype=np.uint8)
+    s_f32 = np.asarray(s_f32, dtype=np.float32)
+    N, K = w.shape
+    full = np.repeat(np.repeat(s_f32, 128, axis=0), 128, axis=1)[:N, :K]
+    with np.errstate(over="ignore", invalid="ignore"):
+        return bf16_round((e4m3fn_decode(w).astype(np.float32) * full).astype(np.float32))
+
+
 # ------------------------------------------------------------------ GEMVs ---
 
 
@@ -175,6 +191,11 @@ def fp8_gemv(x, w, s) -> np.ndarray:
     (runtime/fp8_e4m3_gemv_binding.py:84 contract, dequant of
     runtime/dsv4_engine_mxfp4.py:531-553). x: bf16 bits [K] or [T, K]."""
     return bf16_round(_matvec_f32(fp8_dequant_bf16(w, s), x))
+
+
+def fp8_gemv_f32s(x, w, s_f32) -> np.ndarray:
+    """y = bf16( x @ dequant(W).T ) with fp32 tile scales (fp8_dequant_bf16_f32s)."""
+    return bf16_round(_matvec_f32(fp8_dequant_bf16_f32s(w, s_f32), x))
 
 
 def fp8_gemv_grouped(x, w, s, groups: int) -> np.ndarray:

@@ -25,7 +25,7 @@ LIBS = {
         "mxfp4_moe_routed_dispatch", "mxfp4_moe_grouped_gemv_noalloc", "mxfp4_moe_gate_swiglu"],
     "mxfp4-dense/libmxfp4_gemv.so": ["mxfp4_gemv_m1", "mxfp4_dequant_bf16"],
     "fp8-dense/libfp8_e4m3_gemv.so": ["fp8_e4m3_gemv_m1", "fp8_e4m3_gemv", "fp8_e4m3_gemv_grouped",
-                                      "fp8_e4m3_gemv_multi",
+                                      "fp8_e4m3_gemv_multi", "fp8_e4m3_gemv_f32s",
                                       "fp8_e4m3_swiglu_gemv", "fp8_e4m3_rmsnorm_gemv", "fp8_e4m3_dequant_bf16"],
     "rmsnorm-fuse/librmsnorm_fuse.so": ["rmsnorm_fuse_fwd", "rmsnorm_fuse_residual_add"],
 }
@@ -339,6 +339,15 @@ def test_fp8_validation_codes():
     assert mu(N, 4096, 4096, 0, 2, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -5   # T < 1
     Ns[1] = 0
     assert mu(N, 4096, 4096, 1, 2, ptrs, ptrs, Ns, strides, strides, ptrs, strides, N) == -4   # N < 1
+    fs = lib.fp8_e4m3_gemv_f32s
+    fs.restype = I
+    fs.argtypes = [P, L, P, P, I, I, I, L, L, P, L, P]
+    assert fs(N, 4096, N, N, 4096, 1536, 0, 4096, 32, N, 1536, N) == -5          # T < 1
+    assert fs(N, 4096, N, N, 4000, 1536, 1, 4096, 32, N, 1536, N) == -1          # K % 128
+    assert fs(N, 4096, N, N, 16512, 1536, 1, 16512, 129, N, 1536, N) == -3       # K > 16384
+    D4 = ctypes.c_void_p(1 << 20)
+    assert fs(D4, 4096, D4, ctypes.c_void_p((1 << 20) + 2), 4096, 1536, 1, 4096, 32, D4, 1536, N) == -6  # misaligned
+    assert fs(D4, 4096, D4, D4, 4096, 1536, 1, 4096, 31, D4, 1536, N) == -6      # scale row stride < K/128
     rn = lib.fp8_e4m3_rmsnorm_gemv
     rn.restype = I
     rn.argtypes = [P, P, P, ctypes.c_float, P, P, I, I, I, L, L, P, P, P, P]
@@ -366,6 +375,8 @@ def test_fp8_and_dequant_extensions_reject_null_operands():
             assert fn(*build(ptrs)) == -10, f"{fn.__name__}: pointer {i}"
 
     each_null(fl.fp8_e4m3_gemv, [P, L, P, P, I, I, I, L, L, P, L, P],
+              lambda p: [p[0], 4096, p[1], p[2], 4096, 1536, 2, 4096, 32, p[3], 1536, N], 4)
+    each_null(fl.fp8_e4m3_gemv_f32s, [P, L, P, P, I, I, I, L, L, P, L, P],
               lambda p: [p[0], 4096, p[1], p[2], 4096, 1536, 2, 4096, 32, p[3], 1536, N], 4)
     each_null(fl.fp8_e4m3_gemv_grouped, [P, L, L, P, P, I, I, I, I, L, L, P, L, L, P],
               lambda p: [p[0], 32768, 4096, p[1], p[2], 8, 4096, 1024, 1, 4096, 32, p[3], 8192, 1024, N], 4)

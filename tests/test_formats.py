@@ -141,6 +141,29 @@ def test_fp8_dequant_matches_torch_composition():
     assert np.array_equal(co.fp8_dequant(w, s), got)
 
 
+def test_fp8_dequant_f32_scales_matches_torch_composition():
+    """fp32 tile scales (the benchmark's FP8 configuration): every E4M3FN byte
+    (NaN codes included) against non-power-of-two scales, through torch's
+    float8_e4m3fn view times a float32 tile scale, cast to bfloat16 (the
+    reference's dequantisation, runtime/dsv4_engine_mxfp4.py:539-548)."""
+    w = np.tile(np.arange(256, dtype=np.uint8), (300, 2))           # [300, 512]
+    rng = np.random.default_rng(7)
+    sc = (rng.uniform(0.5, 2.0, (3, 4)) * 2.0 ** rng.integers(-12, 4, (3, 4))).astype(np.float32)
+    wt = torch.from_numpy(w).view(torch.float8_e4m3fn).float()
+    full = torch.from_numpy(sc).repeat_interleave(128, 0).repeat_interleave(128, 1)[:300, :512]
+    ref = (wt * full).to(torch.bfloat16).view(torch.uint16).numpy()
+    got = mx.fp8_dequant_bf16_f32s(w, sc)
+    nan = np.isnan(mx.bf16_to_f32(ref))
+    assert np.array_equal(np.isnan(mx.bf16_to_f32(got)), nan)
+    assert np.array_equal(got[~nan], ref[~nan])
+    # the generator's scales are amax/448 per 128x128 block and its codes in range
+    codes, scales = synth.fp8_weight_f32s(13, 200, 256)
+    assert scales.dtype == np.float32 and scales.shape == (2, 2)
+    deq = mx.bf16_to_f32(mx.fp8_dequant_bf16_f32s(codes, scales))
+    w0 = 0.02 * synth.normal_f64(13, 0, 200 * 256).reshape(200, 256)
+    assert np.abs(deq - w0).max() <= np.abs(w0).max() / 448 * 32 * 1.01   # half an e4m3 step at the top
+
+
 def test_splitmix64_published_outputs():
     # First outputs of SplitMix64 seeded with 0 (Vigna's splitmix64.c).
     want = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 from oracle import mx
 from runtime import fp8_e4m3_gemv_binding as fp8b
@@ -205,3 +206,42 @@ def test_fp8_swiglu_matrix_core_keeps_gemv_bits(device, N, K, T):
     assert g.min() >= 17.0, f"gate sums must be >= 17 for an exact SiLU, min {g.min()}"
     ref = mx.bf16_round((g * mx.bf16_to_f32(up)).astype(np.float32))
     assert np.array_equal(act, ref), f"{int(np.sum(act != ref))} outputs differ from bf16(gate * up)"
+
+
+@pytest.mark.parametrize("N,K", [(1536, 4096), (576, 4096), (4096, 4096), (4096, 2048)])
+@pytest.mark.parametrize("T", [1, 8])
+def test_fp8_gemv_f32_scales_config_shapes(device, N, K, T):
+    """fp8_e4m3_gemv_f32s at the benchmark's FP8 shapes with its literal scale
+    format (one fp32 scale per 128x128 block, amax / 448): against the oracle's
+    dequantise (fp32 product, bf16) then fp32 matmul."""
+    announce(f"fp8_e4m3_gemv_f32s N={N} K={K} T={T}")
+    w, s = synth.fp8_weight_f32s(17200 + N + K, N, K)
+    x = synth.normal_bf16(17300 + T, (T, K))
+    xd = dev_bf16(x, device)
+    y = fp8b.fp8_e4m3_gemv_f32s(dev_u8(w, device), torch.from_numpy(s).to(device), xd[0] if T == 1 else xd)
+    assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv_f32s(x, w, s), f"fp8 f32s N={N} K={K} T={T}")
+
+
+@pytest.mark.parametrize("N,K,T,odd", [(1536, 4096, 1, False), (576, 4096, 8, False), (4096, 2048, 1, False),
+                                       (200, 8192, 1, False), (130, 3200, 2, False), (50, 12288, 3, True),
+                                       (45, 4096, 5, True)])
+def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
+    """With fp32 scales equal to the E8M0 ones (2^(b-127)) the fp32-scale entry
+    gives exactly the E8M0 entry's bits wherever both take the vector kernels
+    (tile shapes on the vector path, the general kernel with aligned and
+    unaligned rows): the scale format is the only difference."""
+    announce(f"fp8_e4m3_gemv_f32s vs fp8_e4m3_gemv bits N={N} K={K} T={T} odd={odd}")
+    w, sb = synth.fp8_weight(17400 + N + K + T, N, K)
+    sf = np.ldexp(np.float32(1.0), sb.astype(np.int32) - 127).astype(np.float32)
+    x = synth.normal_bf16(17500 + T, (T, K))
+    xd = dev_bf16(x, device)
+    xin = xd[0] if T == 1 else xd
+    if odd:
+        buf = torch.zeros(N, K + 1, dtype=torch.uint8, device=device)
+        buf[:, :K] = dev_u8(w, device)
+        tw = buf[:, :K]
+    else:
+        tw = dev_u8(w, device)
+    a = host_bits(fp8b.fp8_e4m3_gemv_f32s(tw, torch.from_numpy(sf).to(device), xin))
+    b = host_bits(fp8b.fp8_e4m3_gemv(tw, dev_u8(sb, device), xin))
+    assert np.array_equal(a, b)
