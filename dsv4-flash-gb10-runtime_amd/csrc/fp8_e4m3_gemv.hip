@@ -390,116 +390,141 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t d0, uint32_t d1) {
     return v;
 }
 
-template <int NW, int PASSES, int MAT, int R>
-__device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
-                                              int blk, float (*part)[MAT][16 * R][16]) {
-    constexpr int L = kMmaLoads;
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int r = lane & 15;
-    const int g = lane >> 4;
-    const int n0 = blk * 16 * R;
-    // Activations through a buffer bounded at the T token rows: the lanes of
-    // token columns T..15 start at the bound and read zeros without touching
-    // memory (their outputs are dropped), so x costs T rows of loads, not 16.
-    const int xbytes = (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2);   // < 2^31 (use_mfma)
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)gv.x, (short)0, xbytes, 0x00020000);
-    const uint32_t xoff = r < a.T ? (uint32_t)(((int64_t)r * a.xstride + 16 * g) * 2) : (uint32_t)xbytes;
-    const uint8_t* wr[MAT][R];
-    const uint8_t* sr[MAT][R];
+// Per-lane operand pointers of the matrix-core kernels. RR (a divisor of 16)
+// is the number of real rows in each 16-row MFMA block: lane row r loads weight
+// row r % RR, so with RR < 16 the block repeats its RR rows (their extra D
+// rows are never stored) and a workgroup covers RR*R rows. A row's sums do
+// not depend on RR: they are the same MFMAs on the same operands.
+template <int MAT, int R, int SF, int RR>
+struct MmaRows {
+    const uint8_t* w[MAT][R];   // this lane's 16 bytes of its row, k = 0
+    const uint8_t* s[MAT][R];   // the row's tile-scale row (SF = 1: fp32 values)
+};
+
+template <int MAT, int R, int SF, int RR>
+__device__ __forceinline__ MmaRows<MAT, R, SF, RR> mma_rows(const Fp8Args& a, const SwigluArgs& sw,
+                                                            const GroupView& gv, int n0, int r, int g) {
+    static_assert(RR == 16 || RR == 8 || RR == 4 || RR == 2, "real rows per block (a divisor of 16)");
+    static_assert(SF == 0 || MAT == 1, "fp32 tile scales: one matrix");
+    MmaRows<MAT, R, SF, RR> m;
 #pragma unroll
     for (int b = 0; b < R; ++b) {
-        const int64_t gn = gv.row0 + min(n0 + 16 * b + r, a.N - 1);
-        wr[0][b] = a.w + gn * a.wrow + 16 * g;
-        sr[0][b] = a.s + (gn / kTile) * a.srow;
+        const int64_t gn = gv.row0 + min(n0 + RR * b + (r % RR), a.N - 1);
+        const int64_t so = (gn / kTile) * a.srow * (SF == 1 ? 4 : 1);
+        m.w[0][b] = a.w + gn * a.wrow + 16 * g;
+        m.s[0][b] = a.s + so;
         if constexpr (MAT == 2) {
-            wr[1][b] = sw.w3 + gn * a.wrow + 16 * g;
-            sr[1][b] = sw.s3 + (gn / kTile) * a.srow;
+            m.w[1][b] = sw.w3 + gn * a.wrow + 16 * g;
+            m.s[1][b] = sw.s3 + so;
         }
     }
-    // One accumulator per pass: each 512-k block's sum starts from zero, so
-    // a wave of several passes produces exactly the partials that one wave
-    // per block would (the blocks are added in k order at the end).
-    f32x4 acc[PASSES][MAT][R];
+    return m;
+}
+
+// One 512-k block (k0 .. k0+511) of R 16-row blocks against the token
+// columns: every load of the block is issued before the first multiply
+// (loads complete in issue order, so each multiply waits only for its own),
+// then each 128-k tile's 4 MFMAs accumulate into a fresh fp32 tile sum that is
+// scaled and added to acc (fresh zeros on entry).
+template <int MAT, int R, int SF, int RR>
+__device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR>& rows, __amdgpu_buffer_rsrc_t xrs,
+                                           uint32_t xoff, int k0, int g, f32x4 (&acc)[MAT][R]) {
+    constexpr int L = kMmaLoads;
+    // This lane's row: the block's 4 tile scales (SF = 0: bytes packed in a
+    // dword; SF = 1: the fp32 bit patterns).
+    uint32_t s4[MAT][R];
+    uint32_t sf[R][4];
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p)
+    for (int m = 0; m < MAT; ++m)
 #pragma unroll
-        for (int m = 0; m < MAT; ++m)
-#pragma unroll
-            for (int b = 0; b < R; ++b) acc[p][m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int k0 = (wave * PASSES + p) * kMmaK;
-        // This lane's rows: the scale bytes of the pass's 4 k-tiles.
-        uint32_t s4[MAT][R];
-#pragma unroll
-        for (int m = 0; m < MAT; ++m)
-#pragma unroll
-            for (int b = 0; b < R; ++b) {
-                const uint8_t* sp = sr[m][b] + k0 / kTile;
+        for (int b = 0; b < R; ++b) {
+            if constexpr (SF == 0) {
+                const uint8_t* sp = rows.s[m][b] + k0 / kTile;
                 s4[m][b] = (uint32_t)sp[0] | ((uint32_t)sp[1] << 8) | ((uint32_t)sp[2] << 16) |
                            ((uint32_t)sp[3] << 24);
+            } else {
+                const uint32_t* sp = reinterpret_cast<const uint32_t*>(rows.s[m][b]) + k0 / kTile;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sf[b][q] = sp[q];
             }
-        u32x4 xv[L][2];
-        u32x4 wv[MAT][R][L];
-#pragma unroll
-        for (int j = 0; j < L; ++j) {
-            xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u), 0, 0);
-            xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u + 16u), 0, 0);
-#pragma unroll
-            for (int b = 0; b < R; ++b)
-#pragma unroll
-                for (int m = 0; m < MAT; ++m) wv[m][b][j] = ld16_stream(wr[m][b] + k0 + 64 * j);
         }
-        // Every load of the pass is issued before the first multiply (loads
-        // complete in issue order, so each multiply waits only for its own).
-        __builtin_amdgcn_sched_barrier(0);
+    u32x4 xv[L][2];
+    u32x4 wv[MAT][R][L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u), 0, 0);
+        xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u + 16u), 0, 0);
 #pragma unroll
         for (int b = 0; b < R; ++b)
 #pragma unroll
-            for (int m = 0; m < MAT; ++m) {
-                // Rows 4g..4g+3 of the block's D operand: their packed tile scales.
-                uint32_t srow[4];
+            for (int m = 0; m < MAT; ++m) wv[m][b][j] = ld16_stream(rows.w[m][b] + k0 + 64 * j);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < R; ++b)
+#pragma unroll
+        for (int m = 0; m < MAT; ++m) {
+            // Rows 4g..4g+3 of the block's D operand: their tile scales come
+            // from the lanes that loaded those rows.
+            uint32_t srow[4];
+            if constexpr (SF == 0) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     srow[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m][b]);
+            }
 #pragma unroll
-                for (int tile = 0; tile < L / 2; ++tile) {
-                    f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int tile = 0; tile < L / 2; ++tile) {
+                f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const int j = 2 * tile + h;
-                        const bf16x8 a0 = fp8x8_to_bf16x8(wv[m][b][j][0], wv[m][b][j][1]);
-                        const bf16x8 a1 = fp8x8_to_bf16x8(wv[m][b][j][2], wv[m][b][j][3]);
-                        ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
-                        ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
-                    }
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * tile + h;
+                    const bf16x8 a0 = fp8x8_to_bf16x8(wv[m][b][j][0], wv[m][b][j][1]);
+                    const bf16x8 a1 = fp8x8_to_bf16x8(wv[m][b][j][2], wv[m][b][j][3]);
+                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
+                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
+                }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[p][m][b][i] = fmaf(ts[i], e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu), acc[p][m][b][i]);
+                for (int i = 0; i < 4; ++i) {
+                    float sc;
+                    if constexpr (SF == 0) sc = e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu);
+                    else sc = __uint_as_float((uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)sf[b][tile]));
+                    acc[m][b][i] = fmaf(ts[i], sc, acc[m][b][i]);
                 }
             }
-    }
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-#pragma unroll
-        for (int m = 0; m < MAT; ++m)
-#pragma unroll
-            for (int b = 0; b < R; ++b)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) part[wave * PASSES + p][m][16 * b + 4 * g + i][r] = acc[p][m][b][i];
-    __syncthreads();
-    for (int o = t; o < 256 * R; o += 64 * NW) {
-        const int tok = o / (16 * R);
-        const int row = o % (16 * R);
-        if (tok >= a.T || n0 + row >= a.N) continue;
+        }
+}
+
+// Activations through a buffer bounded at the T token rows: the lanes of
+// token columns T..15 start at the bound and read zeros without touching
+// memory (their outputs are dropped), so x costs T rows of loads, not 16.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mma_x_rsrc(const Fp8Args& a, const GroupView& gv, int r,
+                                                            uint32_t& xoff, int g) {
+    const int xbytes = (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2);   // < 2^31 (use_mfma)
+    xoff = r < a.T ? (uint32_t)(((int64_t)r * a.xstride + 16 * g) * 2) : (uint32_t)xbytes;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)gv.x, (short)0, xbytes, 0x00020000);
+}
+
+// The workgroup's outputs: the partial sums of nblk 512-k blocks, part[kb],
+// added in k order (kb = 0, 1, ...), then rounded to bf16 (with MAT = 2 the
+// SwiGLU of the two rounded sums).
+template <int MAT, int R, int RR, int NB>
+__device__ __forceinline__ void mma_store(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv, int n0,
+                                          int nblk, int nthreads, const float (*part)[MAT][16 * R][16]) {
+    for (int o = threadIdx.x; o < 16 * RR * R; o += nthreads) {
+        const int tok = o / (RR * R);
+        const int rr = o % (RR * R);
+        const int prow = 16 * (rr / RR) + rr % RR;   // the row's D row in its 16-row block
+        if (tok >= a.T || n0 + rr >= a.N) continue;
         float sum[MAT];
 #pragma unroll
         for (int m = 0; m < MAT; ++m) {
             sum[m] = 0.f;
+            if constexpr (NB > 0) {
 #pragma unroll
-            for (int w2 = 0; w2 < NW * PASSES; ++w2) sum[m] += part[w2][m][row][tok];
+                for (int kb = 0; kb < NB; ++kb) sum[m] += part[kb][m][prow][tok];
+            } else {
+                for (int kb = 0; kb < nblk; ++kb) sum[m] += part[kb][m][prow][tok];
+            }
         }
         uint16_t out;
         if constexpr (MAT == 2) {
@@ -510,15 +535,84 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
         } else {
             out = f32_to_bf16_bits(sum[0]);
         }
-        gv.y[(int64_t)tok * a.ystride + n0 + row] = out;
+        gv.y[(int64_t)tok * a.ystride + n0 + rr] = out;
     }
 }
 
+template <int NW, int PASSES, int MAT, int R, int SF = 0>
+__device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
+                                              int blk, float (*part)[MAT][16 * R][16]) {
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int n0 = blk * 16 * R;
+    uint32_t xoff;
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, xoff, g);
+    const MmaRows<MAT, R, SF, 16> rows = mma_rows<MAT, R, SF, 16>(a, sw, gv, n0, r, g);
+    // One accumulator per pass: each 512-k block's sum starts from zero, so
+    // a wave of several passes produces exactly the partials that one wave
+    // per block would (the blocks are added in k order at the end).
+    f32x4 acc[PASSES][MAT][R];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+#pragma unroll
+        for (int m = 0; m < MAT; ++m)
+#pragma unroll
+            for (int b = 0; b < R; ++b) acc[p][m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        mma_kblock<MAT, R, SF, 16>(rows, xrs, xoff, (wave * PASSES + p) * kMmaK, g, acc[p]);
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int m = 0; m < MAT; ++m)
+#pragma unroll
+            for (int b = 0; b < R; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) part[wave * PASSES + p][m][16 * b + 4 * g + i][r] = acc[p][m][b][i];
+    __syncthreads();
+    mma_store<MAT, R, 16, NW * PASSES>(a, sw, gv, n0, NW * PASSES, 64 * NW, part);
+}
+
 // One matrix, or G row groups of one matrix (blockIdx.y); grid.x = ceil(N/(16R)).
-template <int NW, int PASSES, int MAT, int R>
+template <int NW, int PASSES, int MAT, int R, int SF = 0>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_mfma_kernel(const Fp8Args a, const SwigluArgs sw) {
     __shared__ float part[NW * PASSES][MAT][16 * R][16];
-    fp8_mfma_body<NW, PASSES, MAT, R>(a, sw, group_view(a), blockIdx.x, part);
+    fp8_mfma_body<NW, PASSES, MAT, R, SF>(a, sw, group_view(a), blockIdx.x, part);
+}
+
+// Rows longer than the tile set (K > 4096, a multiple of 512, at most
+// kLongBlocks blocks of 512 k): the workgroup's waves (blockDim.x / 64 of
+// them) take the 512-k blocks kb = wave, wave + waves, ..., each into a fresh
+// sum, so the partials, and their k-order total, do not depend on the wave
+// count. RR real rows per workgroup (one 16-row MFMA block): fewer than 16
+// spread a short matrix over more workgroups, each reading all of x.
+constexpr int kLongBlocks = 32;
+
+template <int RR, int SF>
+__global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args a) {
+    __shared__ float part[kLongBlocks][1][16][16];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int waves = (int)(blockDim.x >> 6);
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const GroupView gv = group_view(a);
+    const int n0 = (int)blockIdx.x * RR;
+    uint32_t xoff;
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, xoff, g);
+    const MmaRows<1, 1, SF, RR> rows = mma_rows<1, 1, SF, RR>(a, SwigluArgs{}, gv, n0, r, g);
+    const int nblk = a.K / kMmaK;
+    for (int kb = wave; kb < nblk; kb += waves) {
+        f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+        mma_kblock<1, 1, SF, RR>(rows, xrs, xoff, kb * kMmaK, g, acc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[kb][0][4 * g + i][r] = acc[0][0][i];
+    }
+    __syncthreads();
+    mma_store<1, 1, RR, 0>(a, SwigluArgs{}, gv, n0, nblk, (int)blockDim.x, part);
 }
 
 // The matrices of fp8_e4m3_gemv_multi: matrix m owns workgroups
@@ -875,17 +969,17 @@ bool use_mfma(int T, int K, int N, int64_t xstride) {
 // The matrix-core path (T >= 2 on the tile shapes): NW waves of 512 k each,
 // except K = 8192 with two matrices (8 waves of two passes, which keeps the
 // second matrix's registers within the 1,024-thread workgroup's budget).
-template <int MAT, int R>
+template <int MAT, int R, int SF>
 void launch_mfma_r(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
     const dim3 grid((unsigned)((a.N + 16 * R - 1) / (16 * R)), (unsigned)G);
     switch (a.K) {
-        case 1024: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<2, 1, MAT, R>), grid, dim3(128), 0, stream, a, sw); break;
-        case 2048: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<4, 1, MAT, R>), grid, dim3(256), 0, stream, a, sw); break;
-        case 4096: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 1, MAT, R>), grid, dim3(512), 0, stream, a, sw); break;
+        case 1024: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<2, 1, MAT, R, SF>), grid, dim3(128), 0, stream, a, sw); break;
+        case 2048: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<4, 1, MAT, R, SF>), grid, dim3(256), 0, stream, a, sw); break;
+        case 4096: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 1, MAT, R, SF>), grid, dim3(512), 0, stream, a, sw); break;
         default:  // K = 8192, R = 1 only
             if constexpr (R == 1) {
                 if constexpr (MAT == 1)
-                    hipLaunchKernelGGL((fp8_gemv_mfma_kernel<16, 1, 1, 1>), grid, dim3(1024), 0, stream, a, sw);
+                    hipLaunchKernelGGL((fp8_gemv_mfma_kernel<16, 1, 1, 1, SF>), grid, dim3(1024), 0, stream, a, sw);
                 else
                     hipLaunchKernelGGL((fp8_gemv_mfma_kernel<8, 2, 2, 1>), grid, dim3(512), 0, stream, a, sw);
             }
@@ -914,26 +1008,25 @@ int mfma_rows(int T, int K, int N, int mat) {
     return best;
 }
 
-template <int MAT>
+template <int MAT, int SF = 0>
 hipError_t launch_mfma(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_t stream) {
     const int R = mfma_rows(a.T, a.K, a.N, MAT);
     if constexpr (MAT == 1) {
-        if (R == 4) launch_mfma_r<1, 4>(a, sw, G, stream);
-        else if (R == 2) launch_mfma_r<1, 2>(a, sw, G, stream);
-        else launch_mfma_r<1, 1>(a, sw, G, stream);
+        if (R == 4) launch_mfma_r<1, 4, SF>(a, sw, G, stream);
+        else if (R == 2) launch_mfma_r<1, 2, SF>(a, sw, G, stream);
+        else launch_mfma_r<1, 1, SF>(a, sw, G, stream);
     } else {
-        if (R == 2) launch_mfma_r<2, 2>(a, sw, G, stream);
-        else launch_mfma_r<2, 1>(a, sw, G, stream);
+        if (R == 2) launch_mfma_r<2, 2, 0>(a, sw, G, stream);
+        else launch_mfma_r<2, 1, 0>(a, sw, G, stream);
     }
     return hipGetLastError();
 }
 
 // Rows longer than the tile set (K > 4096, K a multiple of 512, not 8192)
-// with several tokens: the matrix-core kernel with one wave per 512-k block
-// (PASSES = 1, up to 15 blocks) or per two blocks (PASSES = 2, an even count
-// up to 32, K <= 16384), so each weight byte is read once for all T tokens.
-// Operands as the tile kernels need them (16-byte aligned rows and
-// activations).
+// with several tokens: fp8_gemv_mfma_long_kernel, so each weight byte is read
+// once for all T tokens. Operands as the tile kernels need them (16-byte
+// aligned rows and activations). Returns the number of 512-k blocks, or 0
+// where the path does not apply.
 int long_mfma_blocks(const Fp8Args& a) {
     const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) && (a.T == 1 || a.xstride % 8 == 0) &&
                     (a.xgroup % 8 == 0);
@@ -941,21 +1034,25 @@ int long_mfma_blocks(const Fp8Args& a) {
         ((int64_t)(a.T - 1) * a.xstride + a.K) * 2 > INT32_MAX)
         return 0;
     const int b = a.K / kMmaK;
-    return (b <= 15 || (b % 2 == 0 && b <= 32)) ? b : 0;
+    return b <= kLongBlocks ? b : 0;
 }
 
+// Real rows per long-row workgroup: 16 from 4096 rows (at least 256
+// workgroups, one per CU), else 8. Measured on MI355X at T = 8 (HIP-graph
+// replay): 2048 x 6144 9.50 us with 16 rows, 8.64 with 8, 15.6 with 4;
+// 1024 x 12288 16.3 / 15.0 / 15.1 us; 4096 x 6144 9.87 / 15.8 / 29.5 us.
+int long_rr(int64_t rows) { return rows >= 4096 ? 16 : 8; }
+
+// One wave per 512-k block up to 16 blocks, else one per two blocks
+// (ceil(blocks / 2) waves).
+template <int SF>
 hipError_t launch_mfma_long(const Fp8Args& a, int blocks, int G, hipStream_t stream) {
-    const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)G);
-    const SwigluArgs sw{};
-#define DSV4_L1(NWV) case NWV: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<NWV, 1, 1, 1>), grid, dim3(64 * NWV), 0, stream, a, sw); break;
-#define DSV4_L2(NWV) case 2 * NWV: hipLaunchKernelGGL((fp8_gemv_mfma_kernel<NWV, 2, 1, 1>), grid, dim3(64 * NWV), 0, stream, a, sw); break;
-    switch (blocks) {
-        DSV4_L1(9) DSV4_L1(10) DSV4_L1(11) DSV4_L1(12) DSV4_L1(13) DSV4_L1(14) DSV4_L1(15)
-        DSV4_L2(8) DSV4_L2(9) DSV4_L2(10) DSV4_L2(11) DSV4_L2(12) DSV4_L2(13) DSV4_L2(14) DSV4_L2(15) DSV4_L2(16)
-        default: return hipErrorInvalidValue;
-    }
-#undef DSV4_L1
-#undef DSV4_L2
+    const int waves = blocks <= 16 ? blocks : (blocks + 1) / 2;
+    const dim3 block((unsigned)(64 * waves));
+    if (long_rr((int64_t)a.N * G) == 8)
+        hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<8, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<16, SF>), dim3((unsigned)((a.N + 15) / 16), (unsigned)G), block, 0, stream, a);
     return hipGetLastError();
 }
 
@@ -982,18 +1079,18 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// SF = 1 (fp32 tile scales) takes the vector kernels only: the tile kernel
-// for the tile shapes, the general kernel otherwise.
+// Both tile-scale formats take the same kernels by the same rules (so
+// equal scales give equal bits).
 template <int SF>
 int launch_sf(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
-    const int long_blocks = SF == 0 ? long_mfma_blocks(a) : 0;
+    const int long_blocks = long_mfma_blocks(a);
     if (tile_ok(a)) {
         const int rows = (int)std::min<int64_t>((int64_t)a.N * G, INT32_MAX);
-        e = (SF == 0 && use_mfma(a.T, a.K, rows, a.xstride)) ? launch_mfma<1>(a, SwigluArgs{}, G, stream)
-                                                            : launch_tile<1, SF>(a, SwigluArgs{}, G, stream);
+        e = use_mfma(a.T, a.K, rows, a.xstride) ? launch_mfma<1, SF>(a, SwigluArgs{}, G, stream)
+                                                : launch_tile<1, SF>(a, SwigluArgs{}, G, stream);
     } else if (long_blocks > 0) {
-        e = launch_mfma_long(a, long_blocks, G, stream);
+        e = launch_mfma_long<SF>(a, long_blocks, G, stream);
     } else {
         const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);
         const dim3 block(64 * kWaves);

@@ -320,10 +320,12 @@ int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_f
  * 132-142, runtime/fp8_e4m3_gemv_binding.py:88) carries E8M0 bytes and the
  * reference's dequantisation (runtime/dsv4_engine_mxfp4.py:531-553) multiplies
  * e4m3(W) by the tile's scale in fp32 before rounding to bf16. The scale
- * multiplies each 16-element partial dot (fp32), so results agree with that
- * dequantise-then-multiply path within fp32/bf16 rounding. Vector kernels
- * only (no matrix-core path). Return codes as fp8_e4m3_gemv, plus -6 for a
- * misaligned scale pointer or a scale row stride below K/128. */
+ * multiplies each 16-element partial dot or 128-k tile sum (fp32), so
+ * results agree with that dequantise-then-multiply path within fp32/bf16
+ * rounding. The kernels and the path rule are fp8_e4m3_gemv's (vector and
+ * matrix-core paths), so power-of-two scales give its bits. Return codes as
+ * fp8_e4m3_gemv, plus -6 for a misaligned scale pointer or a scale row stride
+ * below K/128. */
 int fp8_e4m3_gemv_f32s(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,
                        const float* W_scale, int K, int N, int T, int64_t weight_row_stride_bytes,
                        int64_t scale_row_stride, dsv4_bf16_t* y, int64_t y_row_stride,

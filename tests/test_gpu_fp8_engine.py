@@ -227,9 +227,9 @@ def test_fp8_gemv_f32_scales_config_shapes(device, N, K, T):
                                        (45, 4096, 5, True)])
 def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
     """With fp32 scales equal to the E8M0 ones (2^(b-127)) the fp32-scale entry
-    gives exactly the E8M0 entry's bits wherever both take the vector kernels
-    (tile shapes on the vector path, the general kernel with aligned and
-    unaligned rows): the scale format is the only difference."""
+    gives exactly the E8M0 entry's bits on the vector kernels (tile shapes on
+    the vector path, the general kernel with aligned and unaligned rows): the
+    scale format is the only difference."""
     announce(f"fp8_e4m3_gemv_f32s vs fp8_e4m3_gemv bits N={N} K={K} T={T} odd={odd}")
     w, sb = synth.fp8_weight(17400 + N + K + T, N, K)
     sf = np.ldexp(np.float32(1.0), sb.astype(np.int32) - 127).astype(np.float32)
@@ -245,3 +245,30 @@ def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
     a = host_bits(fp8b.fp8_e4m3_gemv_f32s(tw, torch.from_numpy(sf).to(device), xin))
     b = host_bits(fp8b.fp8_e4m3_gemv(tw, dev_u8(sb, device), xin))
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (16384, 1024, 8), (65536, 1024, 8), (4096, 2048, 3),
+                                   (8192, 2048, 8), (32768, 2048, 8), (4096, 4096, 8), (8192, 4096, 8),
+                                   (16384, 4096, 8), (4100, 8192, 2), (576, 6144, 8), (4100, 5120, 4),
+                                   (100, 12800, 6), (300, 16384, 16)])
+def test_fp8_gemv_f32_scales_matrix_cores_equal_e8m0_bits(device, N, K, T):
+    """The fp32-scale entry takes the matrix cores by the E8M0 entry's rules:
+    every row-block count R (1, 2, 4 at K = 1024, 2048, 4096; K = 8192) and
+    the long-row kernel with 8 and 16 real rows per workgroup, one wave per
+    512-k block or per two (25 blocks: one wave with a single block). With
+    fp32 scales 2^(b-127) equal to the E8M0 bytes b the outputs are the same
+    bits. Weights are filled on the device (finite E4M3 codes of both signs,
+    scale bytes 119..125)."""
+    from runtime import fill
+    announce(f"fp8_e4m3_gemv_f32s vs fp8_e4m3_gemv bits on the matrix cores N={N} K={K} T={T}")
+    w = torch.empty(N, K, dtype=torch.uint8, device=device)
+    fill.fill_uniform_u8(w, 17600 + N + K + T, 0, 0, 255)
+    w.bitwise_and_(0xF7)                      # even exponent fields: no 0x7F / 0xFF (NaN)
+    sb = torch.empty((N + 127) // 128, K // 128, dtype=torch.uint8, device=device)
+    fill.fill_uniform_u8(sb, 17700 + N + K + T, 0, 119, 125)
+    sf = torch.ldexp(torch.ones(sb.shape, dtype=torch.float32, device=device), sb.to(torch.int32) - 127)
+    xd = dev_bf16(synth.normal_bf16(17800 + T, (T, K)), device)
+    a = host_bits(fp8b.fp8_e4m3_gemv_f32s(w, sf, xd))
+    b = host_bits(fp8b.fp8_e4m3_gemv(w, sb, xd))
+    assert np.isfinite(mx.bf16_to_f32(b)).all()
+    assert np.array_equal(a, b), f"{int(np.sum(a != b))} outputs differ"
