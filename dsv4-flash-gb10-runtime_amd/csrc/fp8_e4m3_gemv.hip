@@ -497,10 +497,11 @@ __device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR>& rows, 
 // Activations through a buffer bounded at the T token rows: the lanes of
 // token columns T..15 start at the bound and read zeros without touching
 // memory (their outputs are dropped), so x costs T rows of loads, not 16.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t mma_x_rsrc(const Fp8Args& a, const GroupView& gv, int r,
-                                                            uint32_t& xoff, int g) {
+// Lane token column tok reads token tok's activations from k = koff on.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mma_x_rsrc(const Fp8Args& a, const GroupView& gv, int tok,
+                                                            int koff, uint32_t& xoff, int g) {
     const int xbytes = (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2);   // < 2^31 (use_mfma)
-    xoff = r < a.T ? (uint32_t)(((int64_t)r * a.xstride + 16 * g) * 2) : (uint32_t)xbytes;
+    xoff = tok < a.T ? (uint32_t)(((int64_t)tok * a.xstride + 16 * g + koff) * 2) : (uint32_t)xbytes;
     return __builtin_amdgcn_make_buffer_rsrc((void*)gv.x, (short)0, xbytes, 0x00020000);
 }
 
@@ -549,7 +550,7 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
     const int g = lane >> 4;
     const int n0 = blk * 16 * R;
     uint32_t xoff;
-    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, xoff, g);
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, 0, xoff, g);
     const MmaRows<MAT, R, SF, 16> rows = mma_rows<MAT, R, SF, 16>(a, sw, gv, n0, r, g);
     // One accumulator per pass: each 512-k block's sum starts from zero, so
     // a wave of several passes produces exactly the partials that one wave
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args 
     const GroupView gv = group_view(a);
     const int n0 = (int)blockIdx.x * RR;
     uint32_t xoff;
-    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, xoff, g);
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, 0, xoff, g);
     const MmaRows<1, 1, SF, RR> rows = mma_rows<1, 1, SF, RR>(a, SwigluArgs{}, gv, n0, r, g);
     const int nblk = a.K / kMmaK;
     for (int kb = wave; kb < nblk; kb += waves) {
@@ -613,6 +614,51 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args 
     }
     __syncthreads();
     mma_store<1, 1, RR, 0>(a, SwigluArgs{}, gv, n0, nblk, (int)blockDim.x, part);
+}
+
+// Long rows with few tokens (T <= 16/S): one 16x16x32 MFMA multiplies S
+// 512-k blocks at once. Lane r = 16h/S + q (q < 16/S) supplies A row r as
+// weight row n0 + q at block S*kp + h and B column r as token q at the same
+// block; the D quadrant of rows and columns 16h/S .. 16(h+1)/S - 1 is then
+// block S*kp + h's product for the workgroup's 16/S rows and tokens, and the
+// off-diagonal quadrants (rows of one block against tokens of another) are
+// dropped. A lane holds D rows 4g..4g+3 of column r, so lanes with
+// g / (4/S) == h hold the diagonal. Each block's partial is formed as in
+// fp8_gemv_mfma_long_kernel (same MFMAs per 128-k tile, same tile scales,
+// now taken from the lane that loaded the row at that block), and the
+// partials are added in k order: the results are that kernel's bits, with
+// no repeated rows or zero token columns (half or a quarter of the
+// instructions per output).
+template <int S, int SF>
+__global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args a) {
+    constexpr int RB = 16 / S;                       // rows and tokens per workgroup
+    __shared__ float part[kLongBlocks][1][16][16];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int waves = (int)(blockDim.x >> 6);
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int h = r / RB;
+    const int q = r % RB;
+    const GroupView gv = group_view(a);
+    const int n0 = (int)blockIdx.x * RB;
+    uint32_t xoff;
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, q, kMmaK * h, xoff, g);
+    MmaRows<1, 1, SF, RB> rows = mma_rows<1, 1, SF, RB>(a, SwigluArgs{}, gv, n0, r, g);
+    rows.w[0][0] += kMmaK * h;
+    rows.s[0][0] += (kMmaK / kTile) * h * (SF == 1 ? 4 : 1);
+    const int nq = a.K / (S * kMmaK);
+    for (int kp = wave; kp < nq; kp += waves) {
+        f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+        mma_kblock<1, 1, SF, RB>(rows, xrs, xoff, kp * S * kMmaK, g, acc);
+        if (g / (4 / S) == h) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) part[S * kp + h][0][4 * g + i - RB * h][q] = acc[0][0][i];
+        }
+    }
+    __syncthreads();
+    mma_store<1, 1, RB, 0>(a, SwigluArgs{}, gv, n0, S * nq, (int)blockDim.x, part);
 }
 
 // The matrices of fp8_e4m3_gemv_multi: matrix m owns workgroups
@@ -1037,19 +1083,38 @@ int long_mfma_blocks(const Fp8Args& a) {
     return b <= kLongBlocks ? b : 0;
 }
 
-// Real rows per long-row workgroup: 16 from 4096 rows (at least 256
-// workgroups, one per CU), else 8. Measured on MI355X at T = 8 (HIP-graph
-// replay): 2048 x 6144 9.50 us with 16 rows, 8.64 with 8, 15.6 with 4;
-// 1024 x 12288 16.3 / 15.0 / 15.1 us; 4096 x 6144 9.87 / 15.8 / 29.5 us.
-int long_rr(int64_t rows) { return rows >= 4096 ? 16 : 8; }
+// The long-row kernel: S = 4 (4 rows and up to 4 tokens per workgroup) for
+// T <= 4 and at most 1536 rows, S = 2 (8 rows, up to 8 tokens) for T <= 8
+// below 4096 rows and for T <= 4 at any row count, else one block per MFMA
+// with 16 real rows per workgroup from 4096 rows and 8 below (K must hold a
+// whole number of S-block groups). Measured on MI355X (HIP-graph replay,
+// weights rotated over 512 MB), one block per MFMA -> S = 2 -> S = 4:
+// 1024 x 12288 at T = 8 15.0 -> 11.2 us, T = 4 13.1 -> 9.1 -> 7.0, T = 2
+// 11.8 -> 7.9 -> 5.8; 2048 x 6144 at T = 8 8.65 -> 7.15, T = 4 7.72 -> 6.13
+// (S = 4: 7.06); 576 x 16384 at T = 8 18.8 -> 13.4, T = 4 16.3 -> 10.7 ->
+// 8.2; 3072 x 6144 at T = 8 15.5 -> 11.3; 4096 x 6144 at T = 4 10.1 -> 9.6
+// but at T = 8 10.8 -> 11.4. With one block per MFMA, 16 rows per workgroup
+// against 8 (4096 x 6144, T = 8): 9.87 against 15.8 us; 8 against 16 below
+// 4096 rows (2048 x 6144): 8.64 against 9.50.
+int long_split(int64_t rows, int T, int K) {
+    if (T <= 4 && rows <= 1536 && K % (4 * kMmaK) == 0) return 4;
+    if (T <= 8 && (rows < 4096 || T <= 4) && K % (2 * kMmaK) == 0) return 2;
+    return 1;
+}
 
-// One wave per 512-k block up to 16 blocks, else one per two blocks
-// (ceil(blocks / 2) waves).
+// Waves per workgroup: one per group of S blocks up to 16 groups, else one
+// per two groups.
 template <int SF>
 hipError_t launch_mfma_long(const Fp8Args& a, int blocks, int G, hipStream_t stream) {
-    const int waves = blocks <= 16 ? blocks : (blocks + 1) / 2;
-    const dim3 block((unsigned)(64 * waves));
-    if (long_rr((int64_t)a.N * G) == 8)
+    const int64_t rows = (int64_t)a.N * G;
+    const int S = long_split(rows, a.T, a.K);
+    const int groups = blocks / S;
+    const dim3 block((unsigned)(64 * (groups <= 16 ? groups : (groups + 1) / 2)));
+    if (S == 4)
+        hipLaunchKernelGGL((fp8_gemv_mfma_split_kernel<4, SF>), dim3((unsigned)((a.N + 3) / 4), (unsigned)G), block, 0, stream, a);
+    else if (S == 2)
+        hipLaunchKernelGGL((fp8_gemv_mfma_split_kernel<2, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, 0, stream, a);
+    else if (rows < 4096)
         hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<8, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, 0, stream, a);
     else
         hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<16, SF>), dim3((unsigned)((a.N + 15) / 16), (unsigned)G), block, 0, stream, a);

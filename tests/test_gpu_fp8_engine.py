@@ -249,13 +249,14 @@ def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
 
 @pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (16384, 1024, 8), (65536, 1024, 8), (4096, 2048, 3),
                                    (8192, 2048, 8), (32768, 2048, 8), (4096, 4096, 8), (8192, 4096, 8),
-                                   (16384, 4096, 8), (4100, 8192, 2), (576, 6144, 8), (4100, 5120, 4),
-                                   (100, 12800, 6), (300, 16384, 16)])
+                                   (16384, 4096, 8), (4100, 8192, 2), (576, 6144, 8), (1000, 16384, 3),
+                                   (100, 12800, 6), (300, 16384, 16), (4100, 6144, 8)])
 def test_fp8_gemv_f32_scales_matrix_cores_equal_e8m0_bits(device, N, K, T):
     """The fp32-scale entry takes the matrix cores by the E8M0 entry's rules:
     every row-block count R (1, 2, 4 at K = 1024, 2048, 4096; K = 8192) and
-    the long-row kernel with 8 and 16 real rows per workgroup, one wave per
-    512-k block or per two (25 blocks: one wave with a single block). With
+    every long-row kernel (two and four 512-k blocks per MFMA; one block per
+    MFMA with 8 and 16 real rows per workgroup, 25 blocks leaving one wave a
+    single block). With
     fp32 scales 2^(b-127) equal to the E8M0 bytes b the outputs are the same
     bits. Weights are filled on the device (finite E4M3 codes of both signs,
     scale bytes 119..125)."""
