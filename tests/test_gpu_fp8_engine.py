@@ -224,11 +224,16 @@ def test_fp8_gemv_f32_scales_config_shapes(device, N, K, T):
 
 @pytest.mark.parametrize("N,K,T,odd", [(1536, 4096, 1, False), (576, 4096, 8, False), (4096, 2048, 1, False),
                                        (200, 8192, 1, False), (130, 3200, 2, False), (50, 12288, 3, True),
-                                       (45, 4096, 5, True)])
+                                       (45, 4096, 5, True)]
+                         + [(200, K, T, False) for K in (1024, 2048, 4096) for T in (1, 2, 3, 5, 9)]
+                         + [(90, K, T, odd) for K in (384, 1536, 2560) for T in (1, 2) for odd in (False, True)]
+                         + [(70, 12288, 1, False)])
 def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
     """With fp32 scales equal to the E8M0 ones (2^(b-127)) the fp32-scale entry
-    gives exactly the E8M0 entry's bits on the vector kernels (tile shapes on
-    the vector path, the general kernel with aligned and unaligned rows): the
+    gives exactly the E8M0 entry's bits on the vector kernels: the tile kernel
+    at K = 1024, 2048 and 4096 for every token group (T = 1, 2, 3, 5, 9) and
+    K = 8192 at T = 1, the general kernel with one to three 1 KiB chunks per
+    lane and with segmented rows (K = 12288), aligned and unaligned. The
     scale format is the only difference."""
     announce(f"fp8_e4m3_gemv_f32s vs fp8_e4m3_gemv bits N={N} K={K} T={T} odd={odd}")
     w, sb = synth.fp8_weight(17400 + N + K + T, N, K)

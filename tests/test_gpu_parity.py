@@ -682,12 +682,13 @@ def test_moe_prefill_small_vs_oracle(device, T, topk, E):
 
 @pytest.mark.parametrize("K,H,O,T,topk,E", [(1024, 1024, 512, 40, 4, 16), (2048, 1024, 768, 40, 6, 24),
                                              (4096, 2048, 256, 48, 8, 32), (8192, 512, 256, 40, 4, 16),
-                                             (1024, 8192, 256, 40, 4, 16)])
+                                             (1024, 8192, 256, 40, 4, 16), (1024, 4096, 256, 40, 4, 16)])
 def test_moe_prefill_mixed_tiles(device, K, H, O, T, topk, E):
     """The prefill at K = 2048 and 4096 (the unrolled 16- and 32-super-step
-    bodies) and 1024 (the rolled body), and at the reduction cap 8192 on
-    either side (K_in = 8192: rolled stage A with the largest scale tile;
-    hidden = 8192: rolled stage B), with one expert of more than 16 pairs
+    bodies) and 1024 (the rolled body), stage B at hidden = 2048 and 4096
+    (unrolled), and at the reduction cap 8192 on either side (K_in = 8192:
+    rolled stage A with the largest scale tile; hidden = 8192: rolled stage
+    B), with one expert of more than 16 pairs
     (a tile of two or three token blocks) beside one-block tiles: against the oracle,
     deterministic, with a dropped id and a duplicate listing."""
     announce(f"mxfp4_moe_prefill mixed tiles T={T} topk={topk} E={E} K={K} H={H} O={O}")

@@ -294,9 +294,9 @@ def test_fp8_k8192_vector_tiles_far_apart_rows(device):
     """K = 8192 with token rows 2^30 elements (2 GiB) apart: the matrix-core
     kernel reads the activation rows through one buffer of at most 2^31 bytes,
     so these shapes stay on the vector tile kernels with token groups of 2 and
-    4 (single matrix, fused SwiGLU, multi-matrix), called through the C ABI
-    with the row stride. Each against the oracle; the multi-matrix outputs
-    bit for bit against the single GEMV."""
+    4 (single matrix, fused SwiGLU, multi-matrix, fp32 tile scales), called
+    through the C ABI with the row stride. Each against the oracle; the
+    multi-matrix and fp32-scale outputs bit for bit against the single GEMV."""
     import ctypes
     from runtime import _lib as rl
 
@@ -336,5 +336,11 @@ def test_fp8_k8192_vector_tiles_far_apart_rows(device):
         assert rc == 0
         assert np.array_equal(host_bits(ya), single), "multi launch differs from the single launch"
         assert_close(host_bits(yb), mx.fp8_gemv(x[:T], w2, s2), f"multi far rows T={T}")
+        # the fp32-scale entry on the same vector tiles: scales 2^(b-127) give the E8M0 bits
+        sf = torch.from_numpy(np.ldexp(np.float32(1.0), s1.astype(np.int32) - 127).astype(np.float32)).to(device)
+        yf = torch.empty(T, N, dtype=torch.bfloat16, device=device)
+        rc = lib.fp8_e4m3_gemv_f32s(rl.vp(xbuf), stride, rl.vp(d1), rl.vp(sf), K, N, T, K, K // 128, rl.vp(yf), N, st)
+        assert rc == 0
+        assert np.array_equal(host_bits(yf), single), "fp32-scale entry differs from the E8M0 entry"
     del xbuf
     torch.cuda.empty_cache()
