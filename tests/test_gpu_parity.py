@@ -236,14 +236,18 @@ def test_fp8_gemv_long_rows_and_ragged_n(device):
 
 
 @pytest.mark.parametrize("G,N,K,T", [(8, 1024, 4096, 1), (8, 1024, 4096, 3), (8, 1024, 4096, 16), (3, 576, 2048, 2),
-                                     (4, 64, 4096, 1), (2, 200, 1024, 2)])
+                                     (4, 64, 4096, 1), (2, 200, 1024, 2), (3, 100, 6144, 4), (2, 130, 12288, 8),
+                                     (2, 2100, 5120, 8), (2, 60, 7680, 16)])
 def test_fp8_gemv_grouped(device, G, N, K, T):
     """G GEMVs in one launch (the wo_a shape G=8, N=1024, K=4096 first): against
     the oracle, and, for 128-row groups at T = 1 (where a group and a single
     GEMV on its slice both take the vector tile kernel), bit for bit against
     one fp8_e4m3_gemv call per group. At T = 3 the wo_a shape takes the
     matrix cores (its path rule counts all 8,192 rows). N=576 and N=64 put
-    group boundaries inside a scale tile."""
+    group boundaries inside a scale tile. Rows longer than 4096 take the
+    long-row kernels per group: four and two 512-k blocks per MFMA (G=3,
+    N=100, T=4; G=2, N=130, T=8), one block with 16 real rows once the groups
+    hold 4096 rows (G=2, N=2100, T=8) and with 8 (15 blocks, T=16)."""
     announce(f"fp8_e4m3_gemv_grouped G={G} N={N} K={K} T={T}")
     w, s = synth.fp8_weight(4300 + G + N, G * N, K)
     x = synth.normal_bf16(4400 + T, (T, G, K))
