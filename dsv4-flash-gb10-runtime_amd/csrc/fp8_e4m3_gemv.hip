@@ -1068,15 +1068,16 @@ hipError_t launch_mfma(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
     return hipGetLastError();
 }
 
-// Rows longer than the tile set (K > 4096, K a multiple of 512, not 8192)
-// with several tokens: fp8_gemv_mfma_long_kernel, so each weight byte is read
-// once for all T tokens. Operands as the tile kernels need them (16-byte
-// aligned rows and activations). Returns the number of 512-k blocks, or 0
-// where the path does not apply.
+// Rows longer than 4096 (K a multiple of 512) with several tokens: the
+// long-row matrix-core kernels, so each weight byte is read once for all T
+// tokens. Operands as the tile kernels need them (16-byte aligned rows and
+// activations). Returns the number of 512-k blocks, or 0 where the path does
+// not apply. K = 8192, a tile shape, takes it only where it splits blocks
+// across the MFMA (launch_sf).
 int long_mfma_blocks(const Fp8Args& a) {
     const bool al = aligned16(a.x) && aligned16(a.w) && (a.wrow % 16 == 0) && (a.T == 1 || a.xstride % 8 == 0) &&
                     (a.xgroup % 8 == 0);
-    if (!al || a.T < 2 || a.K <= 4096 || a.K % kMmaK != 0 || tile_k(a.K) ||
+    if (!al || a.T < 2 || a.K <= 4096 || a.K % kMmaK != 0 ||
         ((int64_t)(a.T - 1) * a.xstride + a.K) * 2 > INT32_MAX)
         return 0;
     const int b = a.K / kMmaK;
@@ -1146,11 +1147,17 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
 
 // Both tile-scale formats take the same kernels by the same rules (so
 // equal scales give equal bits).
+// K = 8192 takes the split long-row kernel where the long-row rule splits
+// (few rows or tokens; the per-block partials, and so the bits, are those of
+// the one-block matrix-core kernel): 1024 x 8192 at T = 4 5.47 against
+// 9.02 us, 2048 x 8192 at T = 2 6.21 against 8.46, 4096 x 8192 at T = 2
+// 9.70 against 10.09 (HIP-graph replay).
 template <int SF>
 int launch_sf(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
     const int long_blocks = long_mfma_blocks(a);
-    if (tile_ok(a)) {
+    const bool split8192 = a.K == 8192 && long_blocks > 0 && long_split((int64_t)a.N * G, a.T, a.K) > 1;
+    if (tile_ok(a) && !split8192) {
         const int rows = (int)std::min<int64_t>((int64_t)a.N * G, INT32_MAX);
         e = use_mfma(a.T, a.K, rows, a.xstride) ? launch_mfma<1, SF>(a, SwigluArgs{}, G, stream)
                                                 : launch_tile<1, SF>(a, SwigluArgs{}, G, stream);

@@ -255,7 +255,7 @@ def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
 @pytest.mark.parametrize("N,K,T", [(2048, 1024, 4), (16384, 1024, 8), (65536, 1024, 8), (4096, 2048, 3),
                                    (8192, 2048, 8), (32768, 2048, 8), (4096, 4096, 8), (8192, 4096, 8),
                                    (16384, 4096, 8), (4100, 8192, 2), (576, 6144, 8), (1000, 16384, 3),
-                                   (100, 12800, 6), (300, 16384, 16), (4100, 6144, 8)])
+                                   (100, 12800, 6), (300, 16384, 16), (4100, 6144, 8), (1000, 8192, 4), (2048, 8192, 6), (4100, 8192, 6)])
 def test_fp8_gemv_f32_scales_matrix_cores_equal_e8m0_bits(device, N, K, T):
     """The fp32-scale entry takes the matrix cores by the E8M0 entry's rules:
     every row-block count R (1, 2, 4 at K = 1024, 2048, 4096; K = 8192) and

@@ -193,7 +193,7 @@ def test_fp8_gemv_general_path(device, N, K, T, odd_stride):
 @pytest.mark.parametrize("N,K,T", [(576, 6144, 8), (1536, 12288, 8), (64, 9216, 5), (4100, 5120, 4),
                                    (575, 6144, 4), (1000, 16384, 3), (300, 10240, 2),
                                    (200, 16384, 16), (130, 4608, 3), (300, 7680, 2), (100, 12800, 6),
-                                   (4100, 6144, 8)])
+                                   (4100, 6144, 8), (1000, 8192, 4), (2048, 8192, 2), (1000, 8192, 8)])
 def test_fp8_gemv_long_rows_matrix_cores(device, N, K, T):
     """Aligned rows longer than the tile set (K a multiple of 512 above 4096,
     other than 8192) with several tokens, every branch of the long-row rule:
@@ -202,7 +202,9 @@ def test_fp8_gemv_long_rows_matrix_cores(device, N, K, T):
     multiple of 2048; 575 rows: a ragged last workgroup), and one block per
     MFMA with 8 real rows per workgroup (T = 16; odd block counts 9, 15 and
     25, the last leaving one wave a single block) or 16 (4100 rows at T = 8).
-    Each weight byte is read once for all tokens; against the oracle."""
+    K = 8192, a tile shape, joins them where the rule splits blocks (1000
+    rows at T = 4 and 8, 2048 rows at T = 2). Each weight byte is read once
+    for all tokens; against the oracle."""
     announce(f"fp8_e4m3_gemv long rows on the matrix cores N={N} K={K} T={T}")
     w, s = synth.fp8_weight(4700 + N + K + T, N, K)
     x = synth.normal_bf16(4800 + T, (T, K))
