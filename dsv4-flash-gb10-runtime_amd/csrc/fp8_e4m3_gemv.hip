@@ -390,47 +390,78 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t d0, uint32_t d1) {
     return v;
 }
 
-// Per-lane operand pointers of the matrix-core kernels. RR (a divisor of 16)
-// is the number of real rows in each 16-row MFMA block: lane row r loads weight
-// row r % RR, so with RR < 16 the block repeats its RR rows (their extra D
-// rows are never stored) and a workgroup covers RR*R rows. A row's sums do
-// not depend on RR: they are the same MFMAs on the same operands.
-template <int MAT, int R, int SF, int RR>
+// Per-lane operand pointers of the matrix-core kernels. A-operand row rho
+// (0..15) of a 16-row MFMA block is weight row n0 + RR*b + rho % RR at k
+// offset 512 * (rho / RR) when S > 1 (S 512-k blocks per MFMA, RR = 16/S,
+// fp8_gemv_mfma_split_kernel) and at offset 0 otherwise. RR < 16 with S = 1
+// repeats the block's RR rows (their extra D rows are never stored). A row's
+// sums do not depend on RR or S: they are the same MFMAs on the same operands.
+// Weights are loaded as whole 128-byte lines, instruction q (0, 1) of a
+// 128-k chunk giving lane l A-row 8q + l/8 and bytes 16(l%8)..+15 of the
+// chunk (8 lines per instruction, where loads in the MFMA layout would touch
+// 16 half lines), and reach the MFMA layout through the wave's LDS area.
+template <int MAT, int R, int SF, int RR, int S>
 struct MmaRows {
-    const uint8_t* w[MAT][R];   // this lane's 16 bytes of its row, k = 0
-    const uint8_t* s[MAT][R];   // the row's tile-scale row (SF = 1: fp32 values)
+    const uint8_t* lw[MAT][R][2];   // this lane's line piece of A-rows lane/8 and 8 + lane/8, k = 0
+    const uint8_t* s[MAT][R];       // the tile-scale row of this lane's A-row lane%16 (SF = 1: fp32 values)
 };
 
-template <int MAT, int R, int SF, int RR>
-__device__ __forceinline__ MmaRows<MAT, R, SF, RR> mma_rows(const Fp8Args& a, const SwigluArgs& sw,
-                                                            const GroupView& gv, int n0, int r, int g) {
+template <int MAT, int R, int SF, int RR, int S>
+__device__ __forceinline__ MmaRows<MAT, R, SF, RR, S> mma_rows(const Fp8Args& a, const SwigluArgs& sw,
+                                                               const GroupView& gv, int n0, int lane) {
     static_assert(RR == 16 || RR == 8 || RR == 4 || RR == 2, "real rows per block (a divisor of 16)");
+    static_assert(S == 1 || S * RR == 16, "S blocks per MFMA take 16/S rows each");
     static_assert(SF == 0 || MAT == 1, "fp32 tile scales: one matrix");
-    MmaRows<MAT, R, SF, RR> m;
+    constexpr int sb = SF == 1 ? 4 : 1;                 // bytes per scale
+    MmaRows<MAT, R, SF, RR, S> m;
+    const int r = lane & 15;
 #pragma unroll
     for (int b = 0; b < R; ++b) {
         const int64_t gn = gv.row0 + min(n0 + RR * b + (r % RR), a.N - 1);
-        const int64_t so = (gn / kTile) * a.srow * (SF == 1 ? 4 : 1);
-        m.w[0][b] = a.w + gn * a.wrow + 16 * g;
+        const int64_t so = ((gn / kTile) * a.srow + (S > 1 ? (r / RR) * (kMmaK / kTile) : 0)) * sb;
         m.s[0][b] = a.s + so;
-        if constexpr (MAT == 2) {
-            m.w[1][b] = sw.w3 + gn * a.wrow + 16 * g;
-            m.s[1][b] = sw.s3 + so;
+        if constexpr (MAT == 2) m.s[1][b] = sw.s3 + so;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int rho = 8 * q + (lane >> 3);
+            const int64_t gl = gv.row0 + min(n0 + RR * b + (rho % RR), a.N - 1);
+            const int64_t lo = gl * a.wrow + (S > 1 ? (rho / RR) * kMmaK : 0) + 16 * (lane & 7);
+            m.lw[0][b][q] = a.w + lo;
+            if constexpr (MAT == 2) m.lw[1][b][q] = sw.w3 + lo;
         }
     }
     return m;
 }
 
+// LDS operations of one wave run in order; the fences only keep the compiler
+// from moving them across (the staged area is the wave's own, so no barrier).
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kStg = 9;                 // 16-byte slots per staged 128-byte row (144-byte stride)
+constexpr int kStgWave = 16 * kStg;     // the wave's staging area per matrix, in 16-byte slots
+
 // One 512-k block (k0 .. k0+511) of R 16-row blocks against the token
 // columns: every load of the block is issued before the first multiply
 // (loads complete in issue order, so each multiply waits only for its own),
-// then each 128-k tile's 4 MFMAs accumulate into a fresh fp32 tile sum that is
-// scaled and added to acc (fresh zeros on entry).
-template <int MAT, int R, int SF, int RR>
-__device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR>& rows, __amdgpu_buffer_rsrc_t xrs,
-                                           uint32_t xoff, int k0, int g, f32x4 (&acc)[MAT][R]) {
+// then for each 128-k chunk (one scale tile) the wave writes its two weight
+// lines per lane to its staging area stg (matrix m at stg + m * kStgWave:
+// 16 rows of 128 bytes at a 144-byte stride, so the reads of lanes r = 0..15
+// fall in different banks) and reads back, as lane (r, g), row r's bytes
+// 16g and 64 + 16g: the operands the MFMA layout would have loaded. The
+// chunk's 4 MFMAs accumulate into a fresh fp32 tile sum that is scaled and
+// added to acc (fresh zeros on entry). With S = 1 and RR <= 8, A-rows 8..15
+// repeat rows 0..7: only the first line of a chunk is loaded and staged.
+template <int MAT, int R, int SF, int RR, int S>
+__device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR, S>& rows, __amdgpu_buffer_rsrc_t xrs,
+                                           uint32_t xoff, int k0, int lane, u32x4* stg, f32x4 (&acc)[MAT][R]) {
     constexpr int L = kMmaLoads;
-    // This lane's row: the block's 4 tile scales (SF = 0: bytes packed in a
+    constexpr bool HALF = S == 1 && RR <= 8;
+    const int g = lane >> 4;
+    // This lane's A-row: the block's 4 tile scales (SF = 0: bytes packed in a
     // dword; SF = 1: the fp32 bit patterns).
     uint32_t s4[MAT][R];
     uint32_t sf[R][4];
@@ -449,37 +480,46 @@ __device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR>& rows, 
             }
         }
     u32x4 xv[L][2];
-    u32x4 wv[MAT][R][L];
+    u32x4 wl[MAT][R][L];                // line j = 2c + q: chunk c, A-rows 8q + lane/8
 #pragma unroll
     for (int j = 0; j < L; ++j) {
         xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u), 0, 0);
         xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u + 16u), 0, 0);
+        if (HALF && (j & 1)) continue;
 #pragma unroll
         for (int b = 0; b < R; ++b)
 #pragma unroll
-            for (int m = 0; m < MAT; ++m) wv[m][b][j] = ld16_stream(rows.w[m][b] + k0 + 64 * j);
+            for (int m = 0; m < MAT; ++m) wl[m][b][j] = ld16_stream(rows.lw[m][b][j & 1] + k0 + 128 * (j >> 1));
     }
     __builtin_amdgcn_sched_barrier(0);
+    const int wslot = (lane >> 3) * kStg + (lane & 7);               // + 8 * kStg for the second line
+    const int rslot = (HALF ? (lane & 7) : (lane & 15)) * kStg + g;  // + 4 for bytes 64..127
 #pragma unroll
     for (int b = 0; b < R; ++b)
 #pragma unroll
         for (int m = 0; m < MAT; ++m) {
             // Rows 4g..4g+3 of the block's D operand: their tile scales come
-            // from the lanes that loaded those rows.
+            // from the lanes that hold those A-rows.
             uint32_t srow[4];
             if constexpr (SF == 0) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     srow[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m][b]);
             }
+            u32x4* st = stg + m * kStgWave;
 #pragma unroll
             for (int tile = 0; tile < L / 2; ++tile) {
+                wave_lds_order();   // the previous chunk's reads come first
+                st[wslot] = wl[m][b][2 * tile];
+                if constexpr (!HALF) st[wslot + 8 * kStg] = wl[m][b][2 * tile + 1];
+                wave_lds_order();
+                const u32x4 wv[2] = {st[rslot], st[rslot + 4]};
                 f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int j = 2 * tile + h;
-                    const bf16x8 a0 = fp8x8_to_bf16x8(wv[m][b][j][0], wv[m][b][j][1]);
-                    const bf16x8 a1 = fp8x8_to_bf16x8(wv[m][b][j][2], wv[m][b][j][3]);
+                    const bf16x8 a0 = fp8x8_to_bf16x8(wv[h][0], wv[h][1]);
+                    const bf16x8 a1 = fp8x8_to_bf16x8(wv[h][2], wv[h][3]);
                     ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
                     ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
                 }
@@ -540,9 +580,10 @@ __device__ __forceinline__ void mma_store(const Fp8Args& a, const SwigluArgs& sw
     }
 }
 
+// stg: the workgroup's staging areas (MAT * kStgWave slots per wave).
 template <int NW, int PASSES, int MAT, int R, int SF = 0>
 __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
-                                              int blk, float (*part)[MAT][16 * R][16]) {
+                                              int blk, float (*part)[MAT][16 * R][16], u32x4* stg) {
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -551,7 +592,7 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
     const int n0 = blk * 16 * R;
     uint32_t xoff;
     const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, 0, xoff, g);
-    const MmaRows<MAT, R, SF, 16> rows = mma_rows<MAT, R, SF, 16>(a, sw, gv, n0, r, g);
+    const MmaRows<MAT, R, SF, 16, 1> rows = mma_rows<MAT, R, SF, 16, 1>(a, sw, gv, n0, lane);
     // One accumulator per pass: each 512-k block's sum starts from zero, so
     // a wave of several passes produces exactly the partials that one wave
     // per block would (the blocks are added in k order at the end).
@@ -562,7 +603,8 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
         for (int m = 0; m < MAT; ++m)
 #pragma unroll
             for (int b = 0; b < R; ++b) acc[p][m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        mma_kblock<MAT, R, SF, 16>(rows, xrs, xoff, (wave * PASSES + p) * kMmaK, g, acc[p]);
+        mma_kblock<MAT, R, SF, 16, 1>(rows, xrs, xoff, (wave * PASSES + p) * kMmaK, lane,
+                                      stg + wave * MAT * kStgWave, acc[p]);
     }
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
@@ -580,7 +622,8 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
 template <int NW, int PASSES, int MAT, int R, int SF = 0>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_mfma_kernel(const Fp8Args a, const SwigluArgs sw) {
     __shared__ float part[NW * PASSES][MAT][16 * R][16];
-    fp8_mfma_body<NW, PASSES, MAT, R, SF>(a, sw, group_view(a), blockIdx.x, part);
+    __shared__ u32x4 stg[NW * MAT * kStgWave];
+    fp8_mfma_body<NW, PASSES, MAT, R, SF>(a, sw, group_view(a), blockIdx.x, part, stg);
 }
 
 // Rows longer than the tile set (K > 4096, a multiple of 512, at most
@@ -594,6 +637,7 @@ constexpr int kLongBlocks = 32;
 template <int RR, int SF>
 __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args a) {
     __shared__ float part[kLongBlocks][1][16][16];
+    __shared__ u32x4 stg[16 * kStgWave];                // up to 16 waves
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -604,11 +648,11 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args 
     const int n0 = (int)blockIdx.x * RR;
     uint32_t xoff;
     const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, 0, xoff, g);
-    const MmaRows<1, 1, SF, RR> rows = mma_rows<1, 1, SF, RR>(a, SwigluArgs{}, gv, n0, r, g);
+    const MmaRows<1, 1, SF, RR, 1> rows = mma_rows<1, 1, SF, RR, 1>(a, SwigluArgs{}, gv, n0, lane);
     const int nblk = a.K / kMmaK;
     for (int kb = wave; kb < nblk; kb += waves) {
         f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-        mma_kblock<1, 1, SF, RR>(rows, xrs, xoff, kb * kMmaK, g, acc);
+        mma_kblock<1, 1, SF, RR, 1>(rows, xrs, xoff, kb * kMmaK, lane, stg + wave * kStgWave, acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) part[kb][0][4 * g + i][r] = acc[0][0][i];
     }
@@ -633,6 +677,7 @@ template <int S, int SF>
 __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args a) {
     constexpr int RB = 16 / S;                       // rows and tokens per workgroup
     __shared__ float part[kLongBlocks][1][16][16];
+    __shared__ u32x4 stg[16 * kStgWave];                // up to 16 waves
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -645,13 +690,11 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args
     const int n0 = (int)blockIdx.x * RB;
     uint32_t xoff;
     const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, q, kMmaK * h, xoff, g);
-    MmaRows<1, 1, SF, RB> rows = mma_rows<1, 1, SF, RB>(a, SwigluArgs{}, gv, n0, r, g);
-    rows.w[0][0] += kMmaK * h;
-    rows.s[0][0] += (kMmaK / kTile) * h * (SF == 1 ? 4 : 1);
+    const MmaRows<1, 1, SF, RB, S> rows = mma_rows<1, 1, SF, RB, S>(a, SwigluArgs{}, gv, n0, lane);
     const int nq = a.K / (S * kMmaK);
     for (int kp = wave; kp < nq; kp += waves) {
         f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-        mma_kblock<1, 1, SF, RB>(rows, xrs, xoff, kp * S * kMmaK, g, acc);
+        mma_kblock<1, 1, SF, RB, S>(rows, xrs, xoff, kp * S * kMmaK, lane, stg + wave * kStgWave, acc);
         if (g / (4 / S) == h) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) part[S * kp + h][0][4 * g + i - RB * h][q] = acc[0][0][i];
@@ -666,6 +709,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const MultiArgs ma) {
     __shared__ float part[NW][1][16][16];
+    __shared__ u32x4 stg[NW * kStgWave];
     int m = 0;
 #pragma unroll
     for (int j = 1; j < kMaxMulti; ++j) m += (j < ma.n_mats && (int)blockIdx.x >= ma.first[j]) ? 1 : 0;
@@ -678,7 +722,7 @@ __global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const Mult
     a.y = ma.y[m];
     a.ystride = ma.ystride[m];
     const GroupView gv{a.x, a.y, 0};
-    fp8_mfma_body<NW, 1, 1, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part);
+    fp8_mfma_body<NW, 1, 1, 1>(a, SwigluArgs{}, gv, (int)blockIdx.x - ma.first[m], part, stg);
 }
 
 // RMSNorm folded into the GEMV that consumes it (fp8_e4m3_rmsnorm_gemv):
