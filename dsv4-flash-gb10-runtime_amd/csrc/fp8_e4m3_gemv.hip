@@ -404,6 +404,9 @@ template <int MAT, int R, int SF, int RR, int S>
 struct MmaRows {
     const uint8_t* lw[MAT][R][2];   // this lane's line piece of A-rows lane/8 and 8 + lane/8, k = 0
     const uint8_t* s[MAT][R];       // the tile-scale row of this lane's A-row lane%16 (SF = 1: fp32 values)
+    uint32_t xo[2];                 // byte offset in x of this lane's line piece of B-rows lane/8 and 8 + lane/8
+                                    // (k = 0), or the buffer bound (zeros) for a token at or past T
+    bool xq1;                       // B-rows 8..15 hold tokens (S > 1, or T > 8)
 };
 
 template <int MAT, int R, int SF, int RR, int S>
@@ -415,6 +418,16 @@ __device__ __forceinline__ MmaRows<MAT, R, SF, RR, S> mma_rows(const Fp8Args& a,
     constexpr int sb = SF == 1 ? 4 : 1;                 // bytes per scale
     MmaRows<MAT, R, SF, RR, S> m;
     const int r = lane & 15;
+    // B-row rho: token rho (S = 1), or token rho % RR at k offset 512 * (rho / RR).
+    const uint32_t xbytes = (uint32_t)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int rho = 8 * q + (lane >> 3);
+        const int tok = S > 1 ? rho % RR : rho;
+        const int ko = S > 1 ? (rho / RR) * kMmaK : 0;
+        m.xo[q] = tok < a.T ? (uint32_t)(((int64_t)tok * a.xstride + ko) * 2 + 16 * (lane & 7)) : xbytes;
+    }
+    m.xq1 = S > 1 || a.T > 8;
 #pragma unroll
     for (int b = 0; b < R; ++b) {
         const int64_t gn = gv.row0 + min(n0 + RR * b + (r % RR), a.N - 1);
@@ -441,24 +454,33 @@ __device__ __forceinline__ void wave_lds_order() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-constexpr int kStg = 9;                 // 16-byte slots per staged 128-byte row (144-byte stride)
-constexpr int kStgWave = 16 * kStg;     // the wave's staging area per matrix, in 16-byte slots
+constexpr int kStg = 9;                 // 16-byte slots per staged 128-byte weight row (144-byte stride)
+constexpr int kXStg = 17;               // 16-byte slots per staged 256-byte activation row (272-byte stride)
+// A wave's staging area in 16-byte slots: 16 activation rows, then 16 weight
+// rows per matrix.
+constexpr int stg_slots(int mat) { return 16 * kXStg + mat * 16 * kStg; }
 
 // One 512-k block (k0 .. k0+511) of R 16-row blocks against the token
-// columns: every load of the block is issued before the first multiply
-// (loads complete in issue order, so each multiply waits only for its own),
-// then for each 128-k chunk (one scale tile) the wave writes its two weight
-// lines per lane to its staging area stg (matrix m at stg + m * kStgWave:
-// 16 rows of 128 bytes at a 144-byte stride, so the reads of lanes r = 0..15
-// fall in different banks) and reads back, as lane (r, g), row r's bytes
-// 16g and 64 + 16g: the operands the MFMA layout would have loaded. The
-// chunk's 4 MFMAs accumulate into a fresh fp32 tile sum that is scaled and
-// added to acc (fresh zeros on entry). With S = 1 and RR <= 8, A-rows 8..15
-// repeat rows 0..7: only the first line of a chunk is loaded and staged.
+// columns. Every load of the block is issued before the first multiply
+// (loads complete in issue order, so each multiply waits only for its own):
+// per 128-k chunk c (one scale tile) the activation lines of B-rows
+// 8q + lane/8 (bytes 128h + 16(lane%8) of the chunk's 256, h = 0, 1; the
+// second half of the rows only where they hold tokens) and the weight lines
+// of A-rows 8q + lane/8 (bytes 16(lane%8) of the chunk's 128). Then, chunk by
+// chunk, the wave writes them to its staging area stg (activations: 16 rows
+// at a 272-byte stride; weights of matrix m: 16 rows at a 144-byte stride
+// each, reused for every row block) and reads back, as lane (r, g), B-row
+// r's bytes 128h + 32g .. +31 and A-row r's bytes 16g and 64 + 16g: the
+// operands the MFMA layout would have loaded, so the sums are unchanged (the
+// B columns of tokens at or past T read zeros or stale slots, and their D
+// columns are never stored). Each chunk's 4 MFMAs per (matrix, row block)
+// accumulate into a fresh fp32 tile sum that is scaled and added to acc
+// (fresh zeros on entry). With S = 1 and RR <= 8, A-rows 8..15 repeat rows
+// 0..7: only the first weight line of a chunk is loaded and staged.
 template <int MAT, int R, int SF, int RR, int S>
 __device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR, S>& rows, __amdgpu_buffer_rsrc_t xrs,
-                                           uint32_t xoff, int k0, int lane, u32x4* stg, f32x4 (&acc)[MAT][R]) {
-    constexpr int L = kMmaLoads;
+                                           int k0, int lane, u32x4* stg, f32x4 (&acc)[MAT][R]) {
+    constexpr int kChunks = kMmaK / kTile;
     constexpr bool HALF = S == 1 && RR <= 8;
     const int g = lane >> 4;
     // This lane's A-row: the block's 4 tile scales (SF = 0: bytes packed in a
@@ -479,69 +501,92 @@ __device__ __forceinline__ void mma_kblock(const MmaRows<MAT, R, SF, RR, S>& row
                 for (int q = 0; q < 4; ++q) sf[b][q] = sp[q];
             }
         }
-    u32x4 xv[L][2];
-    u32x4 wl[MAT][R][L];                // line j = 2c + q: chunk c, A-rows 8q + lane/8
+    u32x4 xl[kChunks][2][2];            // chunk, row half q, byte half h
+    u32x4 wl[MAT][R][kChunks][2];       // chunk, row half q
+    const bool xq1 = rows.xq1;
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-        xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u), 0, 0);
-        xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(xoff + (uint32_t)(k0 + 64 * j) * 2u + 16u), 0, 0);
-        if (HALF && (j & 1)) continue;
+    for (int c = 0; c < kChunks; ++c) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if (q == 1 && !xq1) continue;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                xl[c][q][h] = __builtin_amdgcn_raw_buffer_load_b128(
+                    xrs, (int)(rows.xo[q] + (uint32_t)(k0 + kTile * c) * 2u + 128u * h), 0, 0);
+        }
 #pragma unroll
         for (int b = 0; b < R; ++b)
 #pragma unroll
-            for (int m = 0; m < MAT; ++m) wl[m][b][j] = ld16_stream(rows.lw[m][b][j & 1] + k0 + 128 * (j >> 1));
+            for (int m = 0; m < MAT; ++m)
+#pragma unroll
+                for (int q = 0; q < (HALF ? 1 : 2); ++q)
+                    wl[m][b][c][q] = ld16_stream(rows.lw[m][b][q] + k0 + kTile * c);
     }
     __builtin_amdgcn_sched_barrier(0);
-    const int wslot = (lane >> 3) * kStg + (lane & 7);               // + 8 * kStg for the second line
-    const int rslot = (HALF ? (lane & 7) : (lane & 15)) * kStg + g;  // + 4 for bytes 64..127
+    // Rows 4g..4g+3 of each block's D operand: their tile scales come from
+    // the lanes that hold those A-rows.
+    uint32_t srow[MAT][R][4];
+    if constexpr (SF == 0) {
 #pragma unroll
-    for (int b = 0; b < R; ++b)
+        for (int m = 0; m < MAT; ++m)
 #pragma unroll
-        for (int m = 0; m < MAT; ++m) {
-            // Rows 4g..4g+3 of the block's D operand: their tile scales come
-            // from the lanes that hold those A-rows.
-            uint32_t srow[4];
-            if constexpr (SF == 0) {
+            for (int b = 0; b < R; ++b)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    srow[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m][b]);
-            }
-            u32x4* st = stg + m * kStgWave;
+                    srow[m][b][i] = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)s4[m][b]);
+    }
+    u32x4* stx = stg;
+    const int xw = (lane >> 3) * kXStg + (lane & 7);                  // + 8 * kXStg for q = 1, + 8 for h = 1
+    const int xr = (lane & 15) * kXStg + 2 * g;                       // + 8 for bytes 128..255
+    const int wslot = (lane >> 3) * kStg + (lane & 7);                // + 8 * kStg for the second line
+    const int rslot = (HALF ? (lane & 7) : (lane & 15)) * kStg + g;   // + 4 for bytes 64..127
 #pragma unroll
-            for (int tile = 0; tile < L / 2; ++tile) {
-                wave_lds_order();   // the previous chunk's reads come first
-                st[wslot] = wl[m][b][2 * tile];
-                if constexpr (!HALF) st[wslot + 8 * kStg] = wl[m][b][2 * tile + 1];
+    for (int tile = 0; tile < kChunks; ++tile) {
+        wave_lds_order();   // the previous chunk's reads come first
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            stx[xw + 8 * h] = xl[tile][0][h];
+            if (xq1) stx[xw + 8 * kXStg + 8 * h] = xl[tile][1][h];
+        }
+        wave_lds_order();
+        u32x4 xv[2][2];     // [h][e]: B-row r's 16 bytes at 128h + 32g + 16e of the chunk
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) xv[h][e] = stx[xr + 8 * h + e];
+#pragma unroll
+        for (int b = 0; b < R; ++b)
+#pragma unroll
+            for (int m = 0; m < MAT; ++m) {
+                u32x4* st = stg + 16 * kXStg + m * 16 * kStg;
+                wave_lds_order();
+                st[wslot] = wl[m][b][tile][0];
+                if constexpr (!HALF) st[wslot + 8 * kStg] = wl[m][b][tile][1];
                 wave_lds_order();
                 const u32x4 wv[2] = {st[rslot], st[rslot + 4]};
                 f32x4 ts = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const int j = 2 * tile + h;
                     const bf16x8 a0 = fp8x8_to_bf16x8(wv[h][0], wv[h][1]);
                     const bf16x8 a1 = fp8x8_to_bf16x8(wv[h][2], wv[h][3]);
-                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[j][0]), ts, 0, 0, 0);
-                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[j][1]), ts, 0, 0, 0);
+                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, xv[h][0]), ts, 0, 0, 0);
+                    ts = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, xv[h][1]), ts, 0, 0, 0);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     float sc;
-                    if constexpr (SF == 0) sc = e8m0_to_f32((srow[i] >> (8 * tile)) & 0xFFu);
+                    if constexpr (SF == 0) sc = e8m0_to_f32((srow[m][b][i] >> (8 * tile)) & 0xFFu);
                     else sc = __uint_as_float((uint32_t)__builtin_amdgcn_ds_bpermute(4 * (4 * g + i), (int)sf[b][tile]));
                     acc[m][b][i] = fmaf(ts[i], sc, acc[m][b][i]);
                 }
             }
-        }
+    }
 }
 
-// Activations through a buffer bounded at the T token rows: the lanes of
-// token columns T..15 start at the bound and read zeros without touching
-// memory (their outputs are dropped), so x costs T rows of loads, not 16.
-// Lane token column tok reads token tok's activations from k = koff on.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t mma_x_rsrc(const Fp8Args& a, const GroupView& gv, int tok,
-                                                            int koff, uint32_t& xoff, int g) {
+// The activation rows through a buffer bounded at the T token rows: lanes
+// whose B-row holds no token read zeros at the bound without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mma_x_buffer(const Fp8Args& a, const GroupView& gv) {
     const int xbytes = (int)(((int64_t)(a.T - 1) * a.xstride + a.K) * 2);   // < 2^31 (use_mfma)
-    xoff = tok < a.T ? (uint32_t)(((int64_t)tok * a.xstride + 16 * g + koff) * 2) : (uint32_t)xbytes;
     return __builtin_amdgcn_make_buffer_rsrc((void*)gv.x, (short)0, xbytes, 0x00020000);
 }
 
@@ -580,7 +625,7 @@ __device__ __forceinline__ void mma_store(const Fp8Args& a, const SwigluArgs& sw
     }
 }
 
-// stg: the workgroup's staging areas (MAT * kStgWave slots per wave).
+// stg: the workgroup's staging areas (stg_slots(MAT) per wave).
 template <int NW, int PASSES, int MAT, int R, int SF = 0>
 __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs& sw, const GroupView& gv,
                                               int blk, float (*part)[MAT][16 * R][16], u32x4* stg) {
@@ -590,8 +635,7 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
     const int r = lane & 15;
     const int g = lane >> 4;
     const int n0 = blk * 16 * R;
-    uint32_t xoff;
-    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, 0, xoff, g);
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_buffer(a, gv);
     const MmaRows<MAT, R, SF, 16, 1> rows = mma_rows<MAT, R, SF, 16, 1>(a, sw, gv, n0, lane);
     // One accumulator per pass: each 512-k block's sum starts from zero, so
     // a wave of several passes produces exactly the partials that one wave
@@ -603,8 +647,8 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
         for (int m = 0; m < MAT; ++m)
 #pragma unroll
             for (int b = 0; b < R; ++b) acc[p][m][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        mma_kblock<MAT, R, SF, 16, 1>(rows, xrs, xoff, (wave * PASSES + p) * kMmaK, lane,
-                                      stg + wave * MAT * kStgWave, acc[p]);
+        mma_kblock<MAT, R, SF, 16, 1>(rows, xrs, (wave * PASSES + p) * kMmaK, lane, stg + wave * stg_slots(MAT),
+                                      acc[p]);
     }
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
@@ -622,7 +666,7 @@ __device__ __forceinline__ void fp8_mfma_body(const Fp8Args& a, const SwigluArgs
 template <int NW, int PASSES, int MAT, int R, int SF = 0>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_mfma_kernel(const Fp8Args a, const SwigluArgs sw) {
     __shared__ float part[NW * PASSES][MAT][16 * R][16];
-    __shared__ u32x4 stg[NW * MAT * kStgWave];
+    __shared__ u32x4 stg[NW * stg_slots(MAT)];
     fp8_mfma_body<NW, PASSES, MAT, R, SF>(a, sw, group_view(a), blockIdx.x, part, stg);
 }
 
@@ -637,7 +681,7 @@ constexpr int kLongBlocks = 32;
 template <int RR, int SF>
 __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args a) {
     __shared__ float part[kLongBlocks][1][16][16];
-    __shared__ u32x4 stg[16 * kStgWave];                // up to 16 waves
+    __shared__ u32x4 stg[16 * stg_slots(1)];            // up to 16 waves
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -646,13 +690,12 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args 
     const int g = lane >> 4;
     const GroupView gv = group_view(a);
     const int n0 = (int)blockIdx.x * RR;
-    uint32_t xoff;
-    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, r, 0, xoff, g);
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_buffer(a, gv);
     const MmaRows<1, 1, SF, RR, 1> rows = mma_rows<1, 1, SF, RR, 1>(a, SwigluArgs{}, gv, n0, lane);
     const int nblk = a.K / kMmaK;
     for (int kb = wave; kb < nblk; kb += waves) {
         f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-        mma_kblock<1, 1, SF, RR, 1>(rows, xrs, xoff, kb * kMmaK, lane, stg + wave * kStgWave, acc);
+        mma_kblock<1, 1, SF, RR, 1>(rows, xrs, kb * kMmaK, lane, stg + wave * stg_slots(1), acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) part[kb][0][4 * g + i][r] = acc[0][0][i];
     }
@@ -677,7 +720,7 @@ template <int S, int SF>
 __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args a) {
     constexpr int RB = 16 / S;                       // rows and tokens per workgroup
     __shared__ float part[kLongBlocks][1][16][16];
-    __shared__ u32x4 stg[16 * kStgWave];                // up to 16 waves
+    __shared__ u32x4 stg[16 * stg_slots(1)];            // up to 16 waves
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -688,13 +731,12 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args
     const int q = r % RB;
     const GroupView gv = group_view(a);
     const int n0 = (int)blockIdx.x * RB;
-    uint32_t xoff;
-    const __amdgpu_buffer_rsrc_t xrs = mma_x_rsrc(a, gv, q, kMmaK * h, xoff, g);
+    const __amdgpu_buffer_rsrc_t xrs = mma_x_buffer(a, gv);
     const MmaRows<1, 1, SF, RB, S> rows = mma_rows<1, 1, SF, RB, S>(a, SwigluArgs{}, gv, n0, lane);
     const int nq = a.K / (S * kMmaK);
     for (int kp = wave; kp < nq; kp += waves) {
         f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-        mma_kblock<1, 1, SF, RB, S>(rows, xrs, xoff, kp * S * kMmaK, lane, stg + wave * kStgWave, acc);
+        mma_kblock<1, 1, SF, RB, S>(rows, xrs, kp * S * kMmaK, lane, stg + wave * stg_slots(1), acc);
         if (g / (4 / S) == h) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) part[S * kp + h][0][4 * g + i - RB * h][q] = acc[0][0][i];
@@ -709,7 +751,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void fp8_gemv_multi_mfma_kernel(const MultiArgs ma) {
     __shared__ float part[NW][1][16][16];
-    __shared__ u32x4 stg[NW * kStgWave];
+    __shared__ u32x4 stg[NW * stg_slots(1)];
     int m = 0;
 #pragma unroll
     for (int j = 1; j < kMaxMulti; ++j) m += (j < ma.n_mats && (int)blockIdx.x >= ma.first[j]) ? 1 : 0;
