@@ -680,8 +680,10 @@ constexpr int kLongBlocks = 32;
 
 template <int RR, int SF>
 __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args a) {
-    __shared__ float part[kLongBlocks][1][16][16];
-    __shared__ u32x4 stg[16 * stg_slots(1)];            // up to 16 waves
+    // long_lds_bytes: the partials of the K/512 blocks, then the waves' staging areas
+    extern __shared__ __align__(16) uint8_t lds[];
+    float (*part)[1][16][16] = reinterpret_cast<float (*)[1][16][16]>(lds);
+    u32x4* stg = reinterpret_cast<u32x4*>(lds + (a.K / kMmaK) * 16 * 16 * 4);
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -719,8 +721,9 @@ __global__ __launch_bounds__(1024) void fp8_gemv_mfma_long_kernel(const Fp8Args 
 template <int S, int SF>
 __global__ __launch_bounds__(1024) void fp8_gemv_mfma_split_kernel(const Fp8Args a) {
     constexpr int RB = 16 / S;                       // rows and tokens per workgroup
-    __shared__ float part[kLongBlocks][1][16][16];
-    __shared__ u32x4 stg[16 * stg_slots(1)];            // up to 16 waves
+    extern __shared__ __align__(16) uint8_t lds[];      // as fp8_gemv_mfma_long_kernel
+    float (*part)[1][16][16] = reinterpret_cast<float (*)[1][16][16]>(lds);
+    u32x4* stg = reinterpret_cast<u32x4*>(lds + (a.K / kMmaK) * 16 * 16 * 4);
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -1072,30 +1075,36 @@ hipError_t launch_tile(const Fp8Args& a, const SwigluArgs& sw, int G, hipStream_
 }
 
 // The matrix-core path replaces the vector tile kernels once the per-token
-// dots outweigh its fixed costs. Its 16-row workgroups cover a matrix with
-// N/16 workgroups, and each wave load spans 16 rows x 64 B, so at small N or
-// few tokens the vector kernels (more workgroups, 1 KiB row loads) are
-// faster, and the longer the rows the more tokens it takes for the matrix
-// cores to win. Measured on MI355X (graph replay over 512 MB of rotated
-// weights; N = 576 .. 8192, K = 1024 .. 4096, T = 2 .. 16) the crossover is
-//   K = 1024: T >= 3 at N >= 2048, T >= 5 at N >= 1024;
-//   K = 2048: T >= 3 at N >= 4096, T >= 5 at N >= 1536;
-//   K = 4096: T >= 3 at N >= 4096, T >= 9 at N >= 1536;
+// dots outweigh its fixed costs: at small N or few tokens the vector kernels
+// (more workgroups, no transposition through LDS) are faster, and the longer
+// the rows the more tokens it takes for the matrix cores to win. Measured on
+// MI355X (graph replay over 512 MB of rotated weights; N = 256 .. 8192,
+// K = 1024 .. 4096, T = 2 .. 16, matrix-core kernels loading whole lines):
+//   K = 1024: T >= 3 at N >= 2048, T >= 5 at any N;
+//   K = 2048: T >= 3 at N >= 4096, T >= 5 at any N;
+//   K = 4096: T >= 3 at N >= 4096, T >= 5 above 512 rows (the split
+//             kernel below 3072 rows up to T = 8: launch_sf; up to 512 rows
+//             the vector kernels have at most one workgroup per CU, 3.43
+//             against 3.83 us at 256 x 4096, T = 5, and 3.64 against 3.96 at
+//             512 rows, T = 8);
 //   K = 8192: T >= 2.
-// The fused SwiGLU and the RMSNorm-folded GEMV apply it to one matrix's
-// rows, so their GEMVs keep the bits of fp8_e4m3_gemv on the same rows. A
-// grouped launch applies it to the rows of all its groups, which is what sets
-// its workgroup count: 8 groups of 1024 x 4096 run on the matrix cores from
-// T = 3 (9.5 against 11.8 us; 13.5 against 31.7 us at T = 16), where a
-// single 1024-row GEMV stays on the vector kernels.
-// The matrix-core kernel reads the T activation rows through one buffer
-// resource, whose byte extent must fit 31 bits.
+// At T <= 4 the boundary is where it was before the line loads (the matrix
+// cores now win there from about 1536 rows at K = 4096, 3072 rows by 25%),
+// because fp8_e4m3_rmsnorm_gemv (T <= 4, K = 2048 or 4096) follows this rule
+// to keep fp8_e4m3_gemv's bits, and on the matrix cores it runs the norm as
+// a launch of its own. The fused SwiGLU and the RMSNorm-folded GEMV apply the
+// rule to one matrix's rows, so their GEMVs keep the bits of fp8_e4m3_gemv on
+// the same rows. A grouped launch applies it to the rows of all its groups,
+// which is what sets its workgroup count: 8 groups of 1024 x 4096 run on the
+// matrix cores from T = 3 (9.5 against 11.8 us; 13.5 against 31.7 us at
+// T = 16). The matrix-core kernels read the T activation rows through one
+// buffer resource, whose byte extent must fit 31 bits.
 bool use_mfma(int T, int K, int N, int64_t xstride) {
     if (T < 2 || ((int64_t)(T - 1) * xstride + K) * 2 > INT32_MAX) return false;
     if (K > 4096) return true;
-    if (K <= 1024) return (T >= 3 && N >= 2048) || (T >= 5 && N >= 1024);
-    if (K <= 2048) return (T >= 3 && N >= 4096) || (T >= 5 && N >= 1536);
-    return (T >= 3 && N >= 4096) || (T >= 9 && N >= 1536);
+    if (K <= 1024) return (T >= 3 && N >= 2048) || T >= 5;
+    if (K <= 2048) return (T >= 3 && N >= 4096) || T >= 5;
+    return (T >= 3 && N >= 4096) || (T >= 5 && N > 512);
 }
 
 // The matrix-core path (T >= 2 on the tile shapes): NW waves of 512 k each,
@@ -1170,41 +1179,58 @@ int long_mfma_blocks(const Fp8Args& a) {
     return b <= kLongBlocks ? b : 0;
 }
 
-// The long-row kernel: S = 4 (4 rows and up to 4 tokens per workgroup) for
-// T <= 4 and at most 1536 rows, S = 2 (8 rows, up to 8 tokens) for T <= 8
-// below 4096 rows and for T <= 4 at any row count, else one block per MFMA
-// with 16 real rows per workgroup from 4096 rows and 8 below (K must hold a
-// whole number of S-block groups). Measured on MI355X (HIP-graph replay,
-// weights rotated over 512 MB), one block per MFMA -> S = 2 -> S = 4:
-// 1024 x 12288 at T = 8 15.0 -> 11.2 us, T = 4 13.1 -> 9.1 -> 7.0, T = 2
-// 11.8 -> 7.9 -> 5.8; 2048 x 6144 at T = 8 8.65 -> 7.15, T = 4 7.72 -> 6.13
-// (S = 4: 7.06); 576 x 16384 at T = 8 18.8 -> 13.4, T = 4 16.3 -> 10.7 ->
-// 8.2; 3072 x 6144 at T = 8 15.5 -> 11.3; 4096 x 6144 at T = 4 10.1 -> 9.6
-// but at T = 8 10.8 -> 11.4. With one block per MFMA, 16 rows per workgroup
-// against 8 (4096 x 6144, T = 8): 9.87 against 15.8 us; 8 against 16 below
-// 4096 rows (2048 x 6144): 8.64 against 9.50.
+// The matrix-core kernel for rows longer than 4096: S = 4 (4 rows and up to
+// 4 tokens per workgroup) for T <= 4 and at most 1024 rows, S = 2 (8 rows, up
+// to 8 tokens) for T <= 8 and at most 2048 rows, else one block per MFMA with
+// 8 real rows per workgroup up to 2048 rows and 16 above (K must hold a whole
+// number of S-block groups). K = 8192, a tile shape, takes these kernels up to
+// 2048 rows and the one-block tile kernel above; K = 4096 takes S = 2 where
+// the matrix cores win below 3072 rows at T = 5 .. 8 (launch_sf).
+// Measured on MI355X (HIP-graph replay, weights rotated over 512 MB; µs, at
+// T = 2 / 4 / 8 / 16):
+//   1024 x 12288: S = 4 5.19 / 5.65, S = 2 6.41 / 6.55 / 7.78, 8 rows 7.55 /
+//   7.79 / 8.62 / 11.3, 16 rows 8.60 / 9.07 / 10.1 / 14.2;
+//   2048 x 12288: S = 2 7.00 / 7.19 / 8.46, S = 4 7.38 / 8.36, 8 rows 8.30 /
+//   8.41 / 9.25 / 12.0, 16 rows 9.15 / 9.66 / 11.0 / 14.8;
+//   3072 x 6144: 16 rows 5.71 / 5.92 / 6.60 / 8.28, S = 2 6.93 / 7.22 /
+//   8.17, 8 rows 8.60 / 8.59 / 9.30 / 12.2;
+//   1536 x 8192: S = 2 5.40 / 5.51 / 6.03, S = 4 5.54 / 6.16, the tile
+//   kernel 5.95 / 6.24 / 7.00 / 9.06, 8 rows 5.67 / 5.81 / 6.25 / 8.28;
+//   3072 x 8192: the tile kernel 6.77 / 7.04 / 7.75 / 9.80, 16 rows 6.87 /
+//   7.16 / 7.97 / 9.97, S = 2 7.91 / 8.12 / 9.55;
+//   2048 x 4096 (T = 5 / 8): S = 2 4.40 / 4.58, the tile kernel 4.60 / 4.86,
+//   vector 6.46 / 6.75; 3072 x 4096: tile 4.95 / 5.12, S = 2 5.58 / 5.96.
 int long_split(int64_t rows, int T, int K) {
-    if (T <= 4 && rows <= 1536 && K % (4 * kMmaK) == 0) return 4;
-    if (T <= 8 && (rows < 4096 || T <= 4) && K % (2 * kMmaK) == 0) return 2;
+    if (T <= 4 && rows <= 1024 && K % (4 * kMmaK) == 0) return 4;
+    if (T <= 8 && rows <= 2048 && K % (2 * kMmaK) == 0) return 2;
     return 1;
 }
 
-// Waves per workgroup: one per group of S blocks up to 16 groups, else one
-// per two groups.
+// Real rows per workgroup of the one-block long-row kernel.
+int long_rr(int64_t rows) { return rows > 2048 ? 16 : 8; }
+
+// Dynamic LDS of the long-row kernels: fp32 partials of every 512-k block
+// (1 KiB each) and each wave's staging area. Sized by the launch, so short
+// rows and few waves leave room for a second workgroup per CU.
+size_t long_lds_bytes(int blocks, int waves) { return (size_t)blocks * 16 * 16 * 4 + (size_t)waves * stg_slots(1) * 16; }
+
+// S blocks per MFMA (1: one block, 8 or 16 real rows by long_rr); waves per
+// workgroup: one per group of S blocks up to 16 groups, else one per two.
 template <int SF>
-hipError_t launch_mfma_long(const Fp8Args& a, int blocks, int G, hipStream_t stream) {
+hipError_t launch_mfma_long(const Fp8Args& a, int blocks, int G, int S, hipStream_t stream) {
     const int64_t rows = (int64_t)a.N * G;
-    const int S = long_split(rows, a.T, a.K);
     const int groups = blocks / S;
-    const dim3 block((unsigned)(64 * (groups <= 16 ? groups : (groups + 1) / 2)));
+    const int waves = groups <= 16 ? groups : (groups + 1) / 2;
+    const dim3 block((unsigned)(64 * waves));
+    const size_t lds = long_lds_bytes(blocks, waves);
     if (S == 4)
-        hipLaunchKernelGGL((fp8_gemv_mfma_split_kernel<4, SF>), dim3((unsigned)((a.N + 3) / 4), (unsigned)G), block, 0, stream, a);
+        hipLaunchKernelGGL((fp8_gemv_mfma_split_kernel<4, SF>), dim3((unsigned)((a.N + 3) / 4), (unsigned)G), block, lds, stream, a);
     else if (S == 2)
-        hipLaunchKernelGGL((fp8_gemv_mfma_split_kernel<2, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, 0, stream, a);
-    else if (rows < 4096)
-        hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<8, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, 0, stream, a);
+        hipLaunchKernelGGL((fp8_gemv_mfma_split_kernel<2, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, lds, stream, a);
+    else if (long_rr(rows) == 8)
+        hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<8, SF>), dim3((unsigned)((a.N + 7) / 8), (unsigned)G), block, lds, stream, a);
     else
-        hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<16, SF>), dim3((unsigned)((a.N + 15) / 16), (unsigned)G), block, 0, stream, a);
+        hipLaunchKernelGGL((fp8_gemv_mfma_long_kernel<16, SF>), dim3((unsigned)((a.N + 15) / 16), (unsigned)G), block, lds, stream, a);
     return hipGetLastError();
 }
 
@@ -1231,24 +1257,25 @@ hipError_t launch_multi(const MultiArgs& ma, int blocks, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Both tile-scale formats take the same kernels by the same rules (so
-// equal scales give equal bits).
-// K = 8192 takes the split long-row kernel where the long-row rule splits
-// (few rows or tokens; the per-block partials, and so the bits, are those of
-// the one-block matrix-core kernel): 1024 x 8192 at T = 4 5.47 against
-// 9.02 us, 2048 x 8192 at T = 2 6.21 against 8.46, 4096 x 8192 at T = 2
-// 9.70 against 10.09 (HIP-graph replay).
+// Both tile-scale formats take the same kernels by the same rules (so equal
+// scales give equal bits). Where use_mfma (or K > 4096) sends a call to the
+// matrix cores, the kernel is the tile kernel or one of the long-row kernels
+// (long_split); all of them form the same per-block partials and add them in
+// k order, so the choice does not change the bits.
 template <int SF>
 int launch_sf(const Fp8Args& a, int G, hipStream_t stream) {
     hipError_t e;
+    const int64_t rows64 = (int64_t)a.N * G;
+    const int rows = (int)std::min<int64_t>(rows64, INT32_MAX);
     const int long_blocks = long_mfma_blocks(a);
-    const bool split8192 = a.K == 8192 && long_blocks > 0 && long_split((int64_t)a.N * G, a.T, a.K) > 1;
-    if (tile_ok(a) && !split8192) {
-        const int rows = (int)std::min<int64_t>((int64_t)a.N * G, INT32_MAX);
-        e = use_mfma(a.T, a.K, rows, a.xstride) ? launch_mfma<1, SF>(a, SwigluArgs{}, G, stream)
-                                                : launch_tile<1, SF>(a, SwigluArgs{}, G, stream);
-    } else if (long_blocks > 0) {
-        e = launch_mfma_long<SF>(a, long_blocks, G, stream);
+    const bool mf = tile_ok(a) && use_mfma(a.T, a.K, rows, a.xstride);
+    int S = 0;      // > 0: a long-row kernel with S blocks per MFMA
+    if (long_blocks > 0 && (a.K != 8192 || rows64 <= 2048)) S = long_split(rows64, a.T, a.K);
+    else if (mf && a.K == 4096 && a.T <= 8 && rows64 < 3072) S = 2;
+    if (S > 0) {
+        e = launch_mfma_long<SF>(a, a.K / kMmaK, G, S, stream);
+    } else if (tile_ok(a)) {
+        e = mf ? launch_mfma<1, SF>(a, SwigluArgs{}, G, stream) : launch_tile<1, SF>(a, SwigluArgs{}, G, stream);
     } else {
         const dim3 grid((unsigned)((a.N + kWaves * kRows - 1) / (kWaves * kRows)), (unsigned)G);
         const dim3 block(64 * kWaves);

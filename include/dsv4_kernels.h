@@ -302,10 +302,13 @@ int fp8_e4m3_gemv_m1(const dsv4_bf16_t* x, const uint8_t* W_fp8, const uint8_t* 
  * y_row_stride elements). With K in {1024, 2048, 4096, 8192} and 16-byte
  * aligned operands it runs on the matrix cores (bf16 MFMA on the exact E4M3
  * values) at K = 8192 from T = 2; at K = 1024 from T = 3 with N >= 2048 and
- * from T = 5 with N >= 1024; at K = 2048 and 4096 from T = 3 with N >= 4096
- * and from T = 5 (K = 2048) or T = 9 (K = 4096) with N >= 1536. Otherwise it
- * runs on the vector units; the two paths agree within fp32 rounding of the
- * sums. Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16
+ * from T = 5 at any N; at K = 2048 from T = 3 with N >= 4096 and from T = 5
+ * at any N; at K = 4096 from T = 3 with N >= 4096 and from T = 5 with
+ * N > 512. Aligned rows longer than 4096 (K a multiple of 512, at most
+ * 16384) take the matrix cores from T = 2. Both need the T activation rows to
+ * span fewer than 2^31 bytes ((T - 1) * x_row_stride + K elements).
+ * Otherwise it runs on the vector units; the two paths agree within fp32
+ * rounding of the sums. Returns as fp8_e4m3_gemv_m1, plus -5 for T<1 or T>16
  * and -10 for a null x, W_fp8, W_scale or y (after the shape checks, before
  * any launch; the other FP8 extensions likewise for their operands). */
 int fp8_e4m3_gemv(const dsv4_bf16_t* x, int64_t x_row_stride, const uint8_t* W_fp8,

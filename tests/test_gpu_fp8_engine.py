@@ -69,13 +69,16 @@ def test_fp8_swiglu_gemv_engine_k(device, N, K, T):
                  f"fp8 swiglu N={N} K={K} T={T}")
 
 
-# Shapes on the matrix-core path (T >= 3 at N >= 4096, or N >= 2048 at
-# K = 1024; T >= 5 at N >= 1536, or N >= 1024 at K = 1024, T >= 9 at K = 4096;
-# T >= 2 at K = 8192) next to the vector path at the same K: every K of the
-# tile set (2, 4, 8 and 16 waves per workgroup), a last 16-row block that is
-# partly past N, and K = 8192 with two matrices (two passes per wave).
+# Shapes on the matrix-core path (K = 1024: T >= 3 at N >= 2048, T >= 5 at
+# any N; K = 2048: T >= 3 at N >= 4096, T >= 5 at any N; K = 4096: T >= 3 at
+# N >= 4096, T >= 5 above 512 rows; K = 8192: T >= 2): every K of the tile
+# set (2, 4, 8 and 16 waves per workgroup), a last 16-row block that is
+# partly past N, K = 4096 below 3072 rows at T = 5 .. 8 (two 512-k blocks per
+# MFMA, a last 8-row workgroup partly past N) and K = 8192 with at most 2048
+# rows (four blocks per MFMA).
 @pytest.mark.parametrize("N,K,T", [(2048, 1024, 8), (2050, 2048, 5), (4096, 2048, 4), (1540, 4096, 9),
-                                   (4100, 4096, 3), (4096, 8192, 16), (64, 8192, 2)])
+                                   (4100, 4096, 3), (4096, 8192, 16), (64, 8192, 2), (600, 4096, 8),
+                                   (2004, 4096, 5)])
 def test_fp8_matrix_core_path(device, N, K, T):
     announce(f"fp8_e4m3_gemv matrix-core path N={N} K={K} T={T}")
     w, s = synth.fp8_weight(16000 + N + K, N, K)
@@ -231,10 +234,13 @@ def test_fp8_gemv_f32_scales_config_shapes(device, N, K, T):
 def test_fp8_gemv_f32_scales_equal_e8m0_bits(device, N, K, T, odd):
     """With fp32 scales equal to the E8M0 ones (2^(b-127)) the fp32-scale entry
     gives exactly the E8M0 entry's bits on the vector kernels: the tile kernel
-    at K = 1024, 2048 and 4096 for every token group (T = 1, 2, 3, 5, 9) and
-    K = 8192 at T = 1, the general kernel with one to three 1 KiB chunks per
-    lane and with segmented rows (K = 12288), aligned and unaligned. The
-    scale format is the only difference."""
+    at K = 1024, 2048 and 4096 for the token groups of 1, 2 and 4 (T = 1, 2,
+    3), at K = 4096 for those of 8 and 16 (T = 5, 9; at K = 1024 and 2048 these
+    shapes take the matrix cores, and the far-apart-rows tests hold the vector
+    kernels' 8- and 16-token groups there) and K = 8192 at T = 1, the general
+    kernel with one to three 1 KiB chunks per lane and with segmented rows
+    (K = 12288), aligned and unaligned. The scale format is the only
+    difference."""
     announce(f"fp8_e4m3_gemv_f32s vs fp8_e4m3_gemv bits N={N} K={K} T={T} odd={odd}")
     w, sb = synth.fp8_weight(17400 + N + K + T, N, K)
     sf = np.ldexp(np.float32(1.0), sb.astype(np.int32) - 127).astype(np.float32)

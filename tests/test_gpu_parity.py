@@ -197,14 +197,14 @@ def test_fp8_gemv_general_path(device, N, K, T, odd_stride):
 def test_fp8_gemv_long_rows_matrix_cores(device, N, K, T):
     """Aligned rows longer than the tile set (K a multiple of 512 above 4096,
     other than 8192) with several tokens, every branch of the long-row rule:
-    two 512-k blocks per MFMA (T <= 8 below 4096 rows, T <= 4 at 4100 rows;
-    K a multiple of 1024), four per MFMA (T <= 4, at most 1536 rows, K a
-    multiple of 2048; 575 rows: a ragged last workgroup), and one block per
-    MFMA with 8 real rows per workgroup (T = 16; odd block counts 9, 15 and
-    25, the last leaving one wave a single block) or 16 (4100 rows at T = 8).
-    K = 8192, a tile shape, joins them where the rule splits blocks (1000
-    rows at T = 4 and 8, 2048 rows at T = 2). Each weight byte is read once
-    for all tokens; against the oracle."""
+    two 512-k blocks per MFMA (T <= 8 at up to 2048 rows, K a multiple of
+    1024), four per MFMA (T <= 4 at up to 1024 rows, K a multiple of 2048;
+    575 rows: a ragged last workgroup), and one block per MFMA with 8 real
+    rows per workgroup up to 2048 rows (T = 16, and block counts 9, 15 and 25
+    that neither split divides, the last leaving one wave a single block) or
+    16 above (4100 rows at T = 4 and 8). K = 8192, a tile shape, joins them
+    at up to 2048 rows (1000 rows at T = 4 and 8, 2048 rows at T = 2). Each
+    weight byte is read once for all tokens; against the oracle."""
     announce(f"fp8_e4m3_gemv long rows on the matrix cores N={N} K={K} T={T}")
     w, s = synth.fp8_weight(4700 + N + K + T, N, K)
     x = synth.normal_bf16(4800 + T, (T, K))
@@ -239,7 +239,7 @@ def test_fp8_gemv_long_rows_and_ragged_n(device):
 
 @pytest.mark.parametrize("G,N,K,T", [(8, 1024, 4096, 1), (8, 1024, 4096, 3), (8, 1024, 4096, 16), (3, 576, 2048, 2),
                                      (4, 64, 4096, 1), (2, 200, 1024, 2), (3, 100, 6144, 4), (2, 130, 12288, 8),
-                                     (2, 2100, 5120, 8), (2, 60, 7680, 16)])
+                                     (2, 2100, 5120, 8), (2, 60, 7680, 16), (2, 700, 4096, 6)])
 def test_fp8_gemv_grouped(device, G, N, K, T):
     """G GEMVs in one launch (the wo_a shape G=8, N=1024, K=4096 first): against
     the oracle, and, for 128-row groups at T = 1 (where a group and a single
@@ -249,7 +249,9 @@ def test_fp8_gemv_grouped(device, G, N, K, T):
     group boundaries inside a scale tile. Rows longer than 4096 take the
     long-row kernels per group: four and two 512-k blocks per MFMA (G=3,
     N=100, T=4; G=2, N=130, T=8), one block with 16 real rows once the groups
-    hold 4096 rows (G=2, N=2100, T=8) and with 8 (15 blocks, T=16)."""
+    hold more than 2048 rows (G=2, N=2100, T=8) and with 8 (15 blocks, T=16).
+    K = 4096 below 3072 rows at T = 5 .. 8 takes two blocks per MFMA as well
+    (G=2, N=700, T=6)."""
     announce(f"fp8_e4m3_gemv_grouped G={G} N={N} K={K} T={T}")
     w, s = synth.fp8_weight(4300 + G + N, G * N, K)
     x = synth.normal_bf16(4400 + T, (T, G, K))

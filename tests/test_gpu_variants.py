@@ -290,43 +290,46 @@ def test_rmsnorm_partial_block_and_scalar_forward(device):
         assert_close(host_bits(y), ry, f"rmsnorm residual H={H}")
 
 
-def test_fp8_k8192_vector_tiles_far_apart_rows(device):
-    """K = 8192 with token rows 2^30 elements (2 GiB) apart: the matrix-core
-    kernel reads the activation rows through one buffer of at most 2^31 bytes,
-    so these shapes stay on the vector tile kernels with token groups of 2 and
-    4 (single matrix, fused SwiGLU, multi-matrix, fp32 tile scales), called
+def _fp8_vector_tiles_far_apart_rows(device, K, Ts, seed):
+    """Token rows just far enough apart that the T rows span more than 2^31
+    bytes: the matrix-core kernels read the activation rows through one buffer
+    of at most 2^31 bytes, so these calls stay on the vector tile kernels
+    (single matrix, fused SwiGLU, multi-matrix, fp32 tile scales), called
     through the C ABI with the row stride. Each against the oracle; the
     multi-matrix and fp32-scale outputs bit for bit against the single GEMV."""
     import ctypes
     from runtime import _lib as rl
 
     lib = fp8b._load_lib()
-    K, N, stride = 8192, 300, 1 << 30
-    T_max = 4
-    announce(f"fp8 K={K} rows {stride} elements apart, T <= {T_max}")
-    x = synth.normal_bf16(21700, (T_max, K))
+    N = 300
+    x = synth.normal_bf16(seed, (max(Ts), K))
     x = mx.bf16_round(8 * mx.bf16_to_f32(x))
-    xbuf = torch.zeros((T_max - 1) * stride + K, dtype=torch.bfloat16, device=device)
     xd = dev_bf16(x, device)
-    for t in range(T_max):
-        xbuf[t * stride:t * stride + K] = xd[t]
-    w1, s1 = synth.fp8_weight(21701, N, K)
-    w3, s3 = synth.fp8_weight(21702, N, K)
-    w2, s2 = synth.fp8_weight(21703, 200, K)
+    w1, s1 = synth.fp8_weight(seed + 1, N, K)
+    w3, s3 = synth.fp8_weight(seed + 2, N, K)
+    w2, s2 = synth.fp8_weight(seed + 3, 200, K)
     d1, e1, d3, e3 = dev_u8(w1, device), dev_u8(s1, device), dev_u8(w3, device), dev_u8(s3, device)
     d2, e2 = dev_u8(w2, device), dev_u8(s2, device)
+    sf = torch.from_numpy(np.ldexp(np.float32(1.0), s1.astype(np.int32) - 127).astype(np.float32)).to(device)
     st = ctypes.c_void_p(rl.stream_ptr(device))
-    for T in (2, 4):
+    for T in Ts:
+        stride = (2**30 // (T - 1) // 8 + 1) * 8            # (T - 1) * stride * 2 bytes > 2^31
+        assert ((T - 1) * stride + K) * 2 > 2**31 - 1
+        announce(f"fp8 K={K} T={T} rows {stride} elements apart")
+        xbuf = torch.zeros((T - 1) * stride + K, dtype=torch.bfloat16, device=device)
+        for t in range(T):
+            xbuf[t * stride:t * stride + K] = xd[t]
         y = torch.empty(T, N, dtype=torch.bfloat16, device=device)
         rc = lib.fp8_e4m3_gemv(rl.vp(xbuf), stride, rl.vp(d1), rl.vp(e1), K, N, T, K, K // 128, rl.vp(y), N, st)
         assert rc == 0
         single = host_bits(y)
-        assert_close(single, mx.fp8_gemv(x[:T], w1, s1), f"fp8 far rows T={T}")
+        assert_close(single, mx.fp8_gemv(x[:T], w1, s1), f"fp8 far rows K={K} T={T}")
         act = torch.empty(T, N, dtype=torch.bfloat16, device=device)
         rc = lib.fp8_e4m3_swiglu_gemv(rl.vp(xbuf), stride, rl.vp(d1), rl.vp(e1), rl.vp(d3), rl.vp(e3), K, N, T,
                                       K, K // 128, 10.0, 1, rl.vp(act), N, st)
         assert rc == 0
-        assert_close(host_bits(act), mx.fp8_swiglu(x[:T], w1, s1, w3, s3, 10.0, True), f"swiglu far rows T={T}")
+        assert_close(host_bits(act), mx.fp8_swiglu(x[:T], w1, s1, w3, s3, 10.0, True),
+                     f"swiglu far rows K={K} T={T}")
         ya = torch.empty(T, N, dtype=torch.bfloat16, device=device)
         yb = torch.empty(T, 200, dtype=torch.bfloat16, device=device)
         PA, IA, LA = ctypes.c_void_p * 2, ctypes.c_int * 2, ctypes.c_int64 * 2
@@ -335,12 +338,26 @@ def test_fp8_k8192_vector_tiles_far_apart_rows(device):
                                      PA(ya.data_ptr(), yb.data_ptr()), LA(N, 200), st)
         assert rc == 0
         assert np.array_equal(host_bits(ya), single), "multi launch differs from the single launch"
-        assert_close(host_bits(yb), mx.fp8_gemv(x[:T], w2, s2), f"multi far rows T={T}")
+        assert_close(host_bits(yb), mx.fp8_gemv(x[:T], w2, s2), f"multi far rows K={K} T={T}")
         # the fp32-scale entry on the same vector tiles: scales 2^(b-127) give the E8M0 bits
-        sf = torch.from_numpy(np.ldexp(np.float32(1.0), s1.astype(np.int32) - 127).astype(np.float32)).to(device)
         yf = torch.empty(T, N, dtype=torch.bfloat16, device=device)
         rc = lib.fp8_e4m3_gemv_f32s(rl.vp(xbuf), stride, rl.vp(d1), rl.vp(sf), K, N, T, K, K // 128, rl.vp(yf), N, st)
         assert rc == 0
         assert np.array_equal(host_bits(yf), single), "fp32-scale entry differs from the E8M0 entry"
-    del xbuf
-    torch.cuda.empty_cache()
+        del xbuf
+        torch.cuda.empty_cache()
+
+
+def test_fp8_k8192_vector_tiles_far_apart_rows(device):
+    """K = 8192 on the vector tile kernels (token groups of 2 and 4, two
+    k-slices per thread): every other shape with T >= 2 at this K takes the
+    matrix cores."""
+    _fp8_vector_tiles_far_apart_rows(device, 8192, (2, 4), 21700)
+
+
+@pytest.mark.parametrize("K", [1024, 2048])
+def test_fp8_short_rows_vector_tiles_far_apart_rows(device, K):
+    """K = 1024 and 2048 with 5 .. 16 tokens on the vector tile kernels (token
+    groups of 8 and 16; the fused SwiGLU in groups of 8 and a last group of
+    1): every other shape with T >= 5 at these K takes the matrix cores."""
+    _fp8_vector_tiles_far_apart_rows(device, K, (5, 9, 16), 21710 + K)
