@@ -87,6 +87,30 @@ def test_fp8_matrix_core_path(device, N, K, T):
     assert_close(host_bits(y).reshape(T, N), mx.fp8_gemv(x, w, s), f"fp8 N={N} K={K} T={T}")
 
 
+@pytest.mark.parametrize("N,K,T", [(1, 1024, 5), (7, 2048, 9), (15, 1024, 16), (17, 2048, 8)])
+def test_fp8_matrix_core_tiny_n(device, N, K, T):
+    """Fewer than 16 rows (and just over 16) on the matrix cores, which take
+    K = 1024 and 2048 from T = 5 at any N: the 16-row block reads its rows
+    clamped to the last one and stores only the real ones. The single GEMV
+    and the fused SwiGLU against the oracle, and a two-matrix launch (N rows
+    and 3 rows) bit for bit against the single GEMVs."""
+    announce(f"fp8_e4m3_gemv matrix-core tiny N={N} K={K} T={T}")
+    w1, s1 = synth.fp8_weight(17900 + N + K, N, K)
+    w3, s3 = synth.fp8_weight(17950 + N + K, N, K)
+    w2, s2 = synth.fp8_weight(17990 + K, 3, K)
+    x = mx.bf16_round(8 * mx.bf16_to_f32(synth.normal_bf16(18000 + T, (T, K))))
+    xd = dev_bf16(x, device)
+    d1, e1 = dev_u8(w1, device), dev_u8(s1, device)
+    d2, e2 = dev_u8(w2, device), dev_u8(s2, device)
+    y = host_bits(fp8b.fp8_e4m3_gemv(d1, e1, xd)).reshape(T, N)
+    assert_close(y, mx.fp8_gemv(x, w1, s1), f"fp8 tiny N={N} K={K} T={T}")
+    act = fp8b.fp8_e4m3_swiglu_gemv(d1, e1, dev_u8(w3, device), dev_u8(s3, device), xd, 10.0, True)
+    assert_close(host_bits(act).reshape(T, N), mx.fp8_swiglu(x, w1, s1, w3, s3, 10.0, True), f"swiglu tiny N={N}")
+    ya, yb = fp8b.fp8_e4m3_gemv_multi([(d1, e1), (d2, e2)], xd)
+    assert np.array_equal(host_bits(ya).reshape(T, N), y)
+    assert np.array_equal(host_bits(yb).reshape(T, 3), host_bits(fp8b.fp8_e4m3_gemv(d2, e2, xd)).reshape(T, 3))
+
+
 @pytest.mark.parametrize("N,K,T", [(8192, 4096, 8), (16384, 4096, 9), (16400, 1024, 16), (8192, 2048, 13),
                                    (8200, 2048, 8), (16400, 4096, 12)])
 def test_fp8_matrix_core_row_blocks(device, N, K, T):
