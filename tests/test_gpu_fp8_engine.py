@@ -35,10 +35,13 @@ def test_fp8_tile_engine_shapes(device, N, K, T):
 
 @pytest.mark.parametrize("shapes,K,T", [([1536, 576], 4096, 1), ([1024, 512], 4096, 1), ([1536, 576], 4096, 4),
                                         ([130, 700, 64], 2048, 2), ([4096, 1024], 8192, 3),
-                                        ([2048, 300], 1024, 1)])
+                                        ([2048, 300], 1024, 1), ([1024, 576], 4096, 8), ([2048, 1024], 4096, 6)])
 def test_fp8_gemv_multi(device, shapes, K, T):
     """Several matrices on one activation in one launch: each output has the
-    bits of fp8_e4m3_gemv on that matrix alone and matches the oracle."""
+    bits of fp8_e4m3_gemv on that matrix alone and matches the oracle. At
+    K = 4096 and T = 6 or 8 the launch runs the matrix-core tile kernel while
+    each matrix alone (below 3072 rows) takes the two-block split kernel: the
+    same per-block partials added in the same order, so the same bits."""
     announce(f"fp8_e4m3_gemv_multi N={shapes} K={K} T={T}")
     mats, dmats = [], []
     for i, N in enumerate(shapes):
